@@ -1,0 +1,205 @@
+"""Benchmark of the Mira mixer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Headline (BASELINE.json `metric`, `configs[1]`): bf16 prefill of the depthwise causal conv
+(width 4) + diagonal decay scan at B=8, T=4096, D=2048 with a carried-in fp32 state, inputs
+resident in HBM. A step is one mira_diag_conv_scan launch over the whole batch; `value` is
+tokens/s over exactly K timed steps. Beside it: the decode leg (`configs[3]`, batch 256,
+128 steps of conv+diag and GLA matrix-state updates), the roofline of the dominant kernel from
+HIP events on the launch stream, and the CPU oracle timed on the host's cores on a bounded
+sample of the same workload. Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "official-mira-llm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "prefill scan tokens/s + % HBM roofline; decode steps/s at batch 256"
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def parse():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--decode-steps", type=int, default=128)
+    return parser.parse_args()
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration), when a summary for this kernel is committed under profiles/."""
+    path = os.path.join(PROFILES, f"{kernel}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as handle:
+        return json.load(handle).get("bytes_per_launch")
+
+
+def prefill_leg(torch, mira, steps, warmup):
+    B, T, D = 8, 4096, 2048
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(B, T, D, device="cuda", generator=g).to(torch.bfloat16)
+    a = torch.sigmoid(torch.rand(B, T, D, device="cuda", generator=g) * 4 + 2).to(torch.bfloat16)
+    w = torch.randn(D, 4, device="cuda", generator=g) * 0.5
+    bias = torch.zeros(D, device="cuda")
+    h0 = torch.randn(B, D, device="cuda", generator=g) * 0.1
+    for _ in range(warmup):
+        mira.diag_conv_scan(x, a, w, bias, h0=h0, return_state=True)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        mira.diag_conv_scan(x, a, w, bias, h0=h0, return_state=True)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    durations = [s.elapsed_time(e) * 1e-3 for s, e in zip(starts, ends)]
+    kernel_s = sum(durations) / len(durations)
+    algorithmic = B * T * D * 6 + B * D * 4 * 2 + D * 4 * 4 + D * 4
+    watchdog = mira.diag_workspace_error()
+    return {
+        "tokens": B * T, "elapsed": elapsed, "kernel_s": kernel_s, "algorithmic": algorithmic,
+        "watchdog": watchdog,
+    }
+
+
+def decode_leg(torch, mira, steps):
+    """256 sequences, one token each per step; per step the conv ring, the
+    diagonal state and the GLA matrix state [256,16,128,128] are read and written in HBM."""
+    B, D, H, d = 256, 2048, 16, 128
+    g = torch.Generator(device="cuda").manual_seed(1)
+    h = torch.randn(B, D, device="cuda", generator=g) * 0.1
+    ring = (torch.randn(B, D, 3, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+    S = torch.randn(B, H, d, d, device="cuda", generator=g) * 0.1
+    xs = torch.randn(steps, B, D, device="cuda", generator=g).to(torch.bfloat16)
+    as_ = torch.sigmoid(torch.rand(steps, B, D, device="cuda", generator=g) * 4 + 2).to(torch.bfloat16)
+    w = torch.randn(D, 4, device="cuda", generator=g) * 0.5
+    qs = torch.nn.functional.normalize(torch.randn(steps, B, H, d, device="cuda", generator=g), dim=-1).bfloat16()
+    ks = torch.nn.functional.normalize(torch.randn(steps, B, H, d, device="cuda", generator=g), dim=-1).bfloat16()
+    vs = torch.randn(steps, B, H, d, device="cuda", generator=g).bfloat16()
+    gs = torch.rand(steps, B, H, device="cuda", generator=g) * -0.099 - 0.001
+    y = torch.empty(B, D, device="cuda", dtype=torch.bfloat16)
+    o = torch.empty(B, H, d, device="cuda", dtype=torch.bfloat16)
+
+    def run(n):
+        for t in range(n):
+            mira.diag_conv_step(xs[t], as_[t], w, None, h, ring, pos=t, out=y)
+            mira.gla_step(qs[t], ks[t], vs[t], gs[t], S, out=o)
+
+    run(4)
+    stream = torch.cuda.current_stream()
+    gla_start = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    gla_end = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(steps):
+        mira.diag_conv_step(xs[t], as_[t], w, None, h, ring, pos=t, out=y)
+        gla_start[t].record(stream)
+        mira.gla_step(qs[t], ks[t], vs[t], gs[t], S, out=o)
+        gla_end[t].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    gla_s = sum(s.elapsed_time(e) for s, e in zip(gla_start, gla_end)) * 1e-3 / steps
+    per_step = (B * H * d * d * 4 * 2 + B * H * d * 2 * 4 + B * H * 4      # GLA state, q k v o, g
+                + B * D * 4 * 2 + B * D * 2 * 3 + B * D * 2 * 3 + B * D * 2)  # h, x a y, ring r+w
+    gla_bytes = B * H * d * d * 4 * 2 + B * H * d * 2 * 4 + B * H * 4
+    return {"steps": steps, "elapsed": elapsed, "per_step_bytes": per_step,
+            "gla_kernel_s": gla_s, "gla_bytes": gla_bytes}
+
+
+def cpu_leg(budget_s=12.0):
+    """The oracle's restatement of the reference CPU mixer (the batched per-token formulation of
+    model/mira_mixer.py:319-387, numpy float32) on the cfg2 workload realised as the K=1 lattice,
+    plus the conv: a bounded sample of 1 sequence x n tokens x 2048 channels."""
+    import numpy as np
+
+    from oracle import baseline as Bl
+    from oracle import lattice as L
+
+    rng = np.random.default_rng(0)
+
+    def run(n):
+        x, a, w, bias, h0 = Bl.diag_inputs(rng, 1, n, 2048, h0_scale=0.1)
+        t0 = time.perf_counter()
+        u = Bl.causal_conv(x, w, bias, dtype=np.float32).astype(np.float32)
+        inputs = Bl.diag_as_lattice(u, a, h0)
+        L.lattice_scan_batched(*inputs[:7], state=inputs[7])
+        return time.perf_counter() - t0
+
+    probe = run(16)
+    n = int(max(16, min(16384, 16 * budget_s / max(probe, 1e-6))))
+    seconds = run(n)
+    return {"value": n / seconds, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 sequence x {n} tokens x 2048 channels (cfg2 geometry, fp32, "
+                      f"oracle batched lattice restatement + conv), {seconds:.1f} s on "
+                      f"{os.cpu_count()} host cores, numpy single-threaded"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the Mira scan shards over "
+                                   "batch and channels with no exchange, and no multi-GPU leg "
+                                   "is built or measured", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from mira_amd import _lib, mira
+
+    if not torch.cuda.is_available() or _lib.library() is None:
+        print(json.dumps({"error": f"needs a HIP device and the built library: {_lib.why()}"}))
+        sys.exit(1)
+    prefill = prefill_leg(torch, mira, args.steps, args.warmup)
+    decode = decode_leg(torch, mira, args.decode_steps)
+    achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
+    traffic = traffic_from_profiles("diag_scan_kernel")
+    gla_achieved = decode["gla_bytes"] / decode["gla_kernel_s"] / 1e9
+    line = {
+        "metric": METRIC,
+        "value": prefill["tokens"] * args.steps / prefill["elapsed"],
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": prefill["elapsed"] / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "cfg2: conv(width 4) + diagonal decay scan prefill, bf16 in/out, "
+                               "fp32 state, B=8 T=4096 D=2048, h0 ~ N(0, 0.1^2)",
+                   "global_batch": 8, "seq_len": 4096, "channels": 2048, "parallelism": "none"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "diag_scan_kernel",
+                     "kernel_us": round(prefill["kernel_s"] * 1e6, 2),
+                     "algorithmic_bytes": prefill["algorithmic"]},
+        "decode": {"metric": "decode steps/s at batch 256", "unit": "steps/s",
+                   "value": decode["steps"] / decode["elapsed"], "steps": decode["steps"],
+                   "bytes_per_step": decode["per_step_bytes"],
+                   "step_GBps": round(decode["per_step_bytes"] * decode["steps"]
+                                      / decode["elapsed"] / 1e9, 1),
+                   "frac_of_hbm": round(decode["per_step_bytes"] * decode["steps"]
+                                        / decode["elapsed"] / 1e9 / HBM_PEAK_GBS, 4),
+                   "gla_step_kernel_us": round(decode["gla_kernel_s"] * 1e6, 2),
+                   "gla_step_GBps": round(gla_achieved, 1)},
+        "watchdog": prefill["watchdog"],
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_leg()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

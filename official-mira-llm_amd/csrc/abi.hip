@@ -1,0 +1,204 @@
+// The C-ABI of libmira_hip.so (declared in include/mira_hip.h): argument checks, error codes and
+// the dispatch to the kernel launchers. Nothing here allocates device memory: workspaces come
+// from the caller.
+#include "mira_device.hpp"
+#include "mira_abi_internal.hpp"
+
+#include <string>
+
+namespace mira {
+
+namespace {
+thread_local std::string g_last_error;
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+int fail(int code, const std::string &message) {
+    g_last_error = message;
+    return code;
+}
+
+int check_launch(const char *what) {
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess)
+        return fail(MIRA_ERR_HIP, std::string(what) + ": " + hipGetErrorString(status));
+    return MIRA_OK;
+}
+
+}  // namespace mira
+
+using namespace mira;
+
+extern "C" {
+
+const char *mira_last_error(void) { return g_last_error.c_str(); }
+
+const char *mira_version(void) { return "mira_hip 0.1 gfx950"; }
+
+int mira_lattice_supported(int K, int M, int dtype) { return lattice_supported(K, M, dtype) ? 1 : 0; }
+
+int mira_lattice_plan_chunk(int B, int T, int C, int K, int M) {
+    if (B <= 0 || T <= 0 || C <= 0 || K <= 0 || M <= 0) return 0;
+    return lattice_plan_chunk(B, T, C, K, M);
+}
+
+size_t mira_lattice_workspace_bytes(int B, int T, int C, int K, int M, int chunk) {
+    if (B <= 0 || T <= 0 || C <= 0 || K <= 0 || M <= 0) return 0;
+    if (chunk <= 0) chunk = lattice_plan_chunk(B, T, C, K, M);
+    return lattice_workspace(B, T, C, K, M, chunk);
+}
+
+static int lattice_common(LatticeArgs &a, int64_t x_row, int64_t alpha_row, int64_t beta_row,
+                          int64_t rho_row, int64_t gamma_row, int64_t read_row) {
+    if (a.B <= 0 || a.T <= 0 || a.C <= 0)
+        return fail(MIRA_ERR_ARG, "mira: requires nonempty batch, token and channel axes");
+    if (!lattice_supported(a.K, a.M, a.dtype))
+        return fail(MIRA_DECLINE, "mira: no kernel for K=" + std::to_string(a.K) +
+                                      " d_m=" + std::to_string(a.M) +
+                                      " dtype=" + std::to_string(a.dtype));
+    if (!arch_valid(a.mode)) return fail(MIRA_ERR_ARG, "mira: unknown arch mode");
+    if (!a.x || !a.alpha || !a.beta || !a.rho || !a.gamma || !a.write || !a.read || !a.out)
+        return fail(MIRA_ERR_ARG, "mira: a required tensor is null");
+    if (x_row < a.C || gamma_row < a.C || alpha_row < (int64_t)a.C * a.K ||
+        beta_row < (int64_t)a.C * a.K || rho_row < (int64_t)a.C * (a.K + 1) ||
+        read_row < (int64_t)(a.K + 1) * a.M)
+        return fail(MIRA_DECLINE, "mira: a row stride is narrower than its row");
+    if (a.state_out && a.state_in && a.state_out == a.state_in && a.T > 1)
+        return fail(MIRA_ERR_ARG, "mira: state_out may not alias state_in over several tokens");
+    a.x_row = x_row; a.alpha_row = alpha_row; a.beta_row = beta_row; a.rho_row = rho_row;
+    a.gamma_row = gamma_row; a.read_row = read_row;
+    return MIRA_OK;
+}
+
+int mira_lattice_forward(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,
+                         const void *beta, int64_t beta_row, const void *rho, int64_t rho_row,
+                         const void *gamma, int64_t gamma_row, const void *memory_write,
+                         const void *memory_read, int64_t read_row, const uint8_t *valid,
+                         const float *state_in, float *state_out, void *out, int B, int T, int C,
+                         int K, int M, int dtype, int arch_mode, int chunk, void *workspace,
+                         size_t workspace_bytes, void *stream) {
+    LatticeArgs a{};
+    a.x = x; a.alpha = alpha; a.beta = beta; a.rho = rho; a.gamma = gamma;
+    a.write = memory_write; a.read = memory_read; a.valid = valid;
+    a.state_in = state_in; a.state_out = state_out; a.out = out;
+    a.B = B; a.T = T; a.C = C; a.K = K; a.M = M; a.dtype = dtype; a.mode = arch_mode;
+    if (int rc = lattice_common(a, x_row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+        return rc;
+    if (chunk <= 0) chunk = lattice_plan_chunk(B, T, C, K, M);
+    if (chunk > T) chunk = T;
+    a.chunk = chunk;
+    a.chunks = (T + chunk - 1) / chunk;
+    const size_t need = lattice_workspace(B, T, C, K, M, chunk);
+    if (need > 0) {
+        if (!workspace || workspace_bytes < need)
+            return fail(MIRA_ERR_ARG, "mira: workspace smaller than mira_lattice_workspace_bytes");
+        const long long planes = (long long)B * a.chunks * C;
+        a.phi = static_cast<float *>(workspace);
+        a.carry = a.phi + planes * K * K;
+    }
+    return lattice_launch(a, static_cast<hipStream_t>(stream));
+}
+
+int mira_lattice_step(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,
+                      const void *beta, int64_t beta_row, const void *rho, int64_t rho_row,
+                      const void *gamma, int64_t gamma_row, const void *memory_write,
+                      const void *memory_read, int64_t read_row, const uint8_t *valid,
+                      const float *state_in, float *state_out, void *out, int B, int C, int K,
+                      int M, int dtype, int arch_mode, void *stream) {
+    LatticeArgs a{};
+    a.x = x; a.alpha = alpha; a.beta = beta; a.rho = rho; a.gamma = gamma;
+    a.write = memory_write; a.read = memory_read; a.valid = valid;
+    a.state_in = state_in; a.state_out = state_out; a.out = out;
+    a.B = B; a.T = 1; a.C = C; a.K = K; a.M = M; a.dtype = dtype; a.mode = arch_mode;
+    if (int rc = lattice_common(a, x_row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+        return rc;
+    a.chunk = 1;
+    a.chunks = 1;
+    return lattice_launch(a, static_cast<hipStream_t>(stream));
+}
+
+size_t mira_diag_workspace_bytes(int B, int T, int D, int dtype) {
+    if (B <= 0 || T <= 0 || D <= 0 || dtype < MIRA_F32 || dtype > MIRA_F16) return 0;
+    return diag_workspace(B, T, D, dtype);
+}
+
+static int diag_common(const DiagArgs &a) {
+    if (a.B <= 0 || a.T <= 0 || a.D <= 0)
+        return fail(MIRA_ERR_ARG, "diag: requires nonempty batch, token and channel axes");
+    if (a.dtype < MIRA_F32 || a.dtype > MIRA_F16) return fail(MIRA_DECLINE, "diag: unsupported dtype");
+    if (a.W != 4) return fail(MIRA_DECLINE, "diag: conv width must be 4");
+    const int vec = 4;
+    if (a.D % vec) return fail(MIRA_DECLINE, "diag: D must be a multiple of 4");
+    if (!a.x || !a.a || !a.w || !a.y) return fail(MIRA_ERR_ARG, "diag: a required tensor is null");
+    if (!aligned16(a.x) || !aligned16(a.a) || !aligned16(a.y))
+        return fail(MIRA_DECLINE, "diag: x, a and y must be 16-byte aligned");
+    if (a.pos < 0) return fail(MIRA_ERR_ARG, "diag: pos must be >= 0");
+    return MIRA_OK;
+}
+
+int mira_diag_conv_scan(const void *x, const void *a, const float *w, const float *bias,
+                        const float *h0, const void *ring_in, void *ring_out, int64_t pos,
+                        void *y, float *hT, int B, int T, int D, int W, int dtype,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+    DiagArgs d{};
+    d.x = x; d.a = a; d.w = w; d.bias = bias; d.h0 = h0; d.ring_in = ring_in; d.ring_out = ring_out;
+    d.pos = pos; d.y = y; d.hT = hT; d.B = B; d.T = T; d.D = D; d.W = W; d.dtype = dtype;
+    if (int rc = diag_common(d)) return rc;
+    if (!workspace) return fail(MIRA_ERR_ARG, "diag: workspace is null");
+    return diag_scan_launch(d, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mira_diag_conv_step(const void *x, const void *a, const float *w, const float *bias,
+                        float *h, void *ring, int64_t pos, void *y, int B, int D, int W,
+                        int dtype, void *stream) {
+    DiagArgs d{};
+    d.x = x; d.a = a; d.w = w; d.bias = bias; d.ring_in = ring; d.ring_out = ring; d.pos = pos;
+    d.y = y; d.B = B; d.T = 1; d.D = D; d.W = W; d.dtype = dtype;
+    if (int rc = diag_common(d)) return rc;
+    if (!h || !aligned16(h)) return fail(MIRA_ERR_ARG, "diag: h must be a 16-byte aligned state");
+    return diag_step_launch(d, h, static_cast<hipStream_t>(stream));
+}
+
+int mira_diag_workspace_error(void *workspace, size_t workspace_bytes, unsigned *value) {
+    return diag_read_error(workspace, workspace_bytes, value);
+}
+
+static int gla_common(const GlaArgs &a) {
+    if (a.B <= 0 || a.T <= 0 || a.H <= 0)
+        return fail(MIRA_ERR_ARG, "gla: requires nonempty batch, token and head axes");
+    if (a.dk != 128 || a.dv != 128) return fail(MIRA_DECLINE, "gla: d_k = d_v = 128 only");
+    if (a.dtype < MIRA_F32 || a.dtype > MIRA_F16) return fail(MIRA_DECLINE, "gla: unsupported dtype");
+    if (!a.q || !a.k || !a.v || !a.g || !a.o) return fail(MIRA_ERR_ARG, "gla: a required tensor is null");
+    if ((a.S0 && !aligned16(a.S0)) || (a.ST && !aligned16(a.ST)))
+        return fail(MIRA_DECLINE, "gla: states must be 16-byte aligned");
+    return MIRA_OK;
+}
+
+size_t mira_gla_workspace_bytes(int B, int T, int H, int dk, int dv) {
+    return gla_workspace(B, T, H, dk, dv);
+}
+
+int mira_gla_chunked(const void *q, const void *k, const void *v, const float *g,
+                     const float *S0, float *ST, void *o, int B, int T, int H, int dk, int dv,
+                     int dtype, void *workspace, size_t workspace_bytes, void *stream) {
+    GlaArgs a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.S0 = S0; a.ST = ST; a.o = o;
+    a.B = B; a.T = T; a.H = H; a.dk = dk; a.dv = dv; a.dtype = dtype;
+    if (int rc = gla_common(a)) return rc;
+    if (workspace_bytes < gla_workspace(B, T, H, dk, dv))
+        return fail(MIRA_ERR_ARG, "gla: workspace smaller than mira_gla_workspace_bytes");
+    return gla_chunked_launch(a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int mira_gla_step(const void *q, const void *k, const void *v, const float *g, float *S,
+                  void *o, int B, int H, int dk, int dv, int dtype, void *stream) {
+    GlaArgs a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.S0 = S; a.ST = S; a.o = o;
+    a.B = B; a.T = 1; a.H = H; a.dk = dk; a.dv = dv; a.dtype = dtype;
+    if (int rc = gla_common(a)) return rc;
+    if (!S) return fail(MIRA_ERR_ARG, "gla: the state is null");
+    return gla_step_launch(a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,378 @@
+// The K-stage matrix lattice scan (the reference operator, model/mira_mixer.py:246-387) on gfx950.
+//
+// Per (b, t, c) and memory slot m, with (rc_k, rs_k) = r_k (cos theta_k, sin theta_k):
+//     U = x[b,t,c] s[b,t,m]
+//     for k = K..1:  level_k = rs_k U + rc_k V^(k-1),   U = rc_k U - rs_k V^(k-1)
+//     level_0 = U,   V^(0..K-1) <- level_(0..K-1)
+//     y[b,t,c] = SiLU(gamma) sum_k rho_k sum_m level_k[m] nu_k[m]
+// A masked token leaves V unchanged and writes 0.
+//
+// Work split (three launches when the token axis is cut, one when it is not):
+//   summary  per (b, chunk, c): the chunk's affine map from a zero state -- Phi [K,K] (the K
+//            basis states pushed through with zero input) and carry [K,M] (the state reached from
+//            zero). The last chunk is never summarised: nothing reads it.
+//   combine  per (b, c, m): S_(j+1) = Phi_j S_j + carry_j over the chunks, writing the state that
+//            enters every chunk over its carry slot.
+//   replay   per (b, chunk, c): the chunk from its entering state with the readout and the gate;
+//            the last chunk stores the final state. With one chunk this is the whole scan, and at
+//            T = 1 it is the decode step.
+// A block is 256 threads = G channels x L lanes; lane l of a channel owns M/L memory slots, so a
+// channel's K x M state lives in registers. The write and read vectors s, nu are per (b, t) and
+// shared by every channel, so a block stages a tile of TT tokens of them in LDS.
+#include "mira_device.hpp"
+#include "mira_abi_internal.hpp"
+
+#include <algorithm>
+
+namespace mira {
+namespace {
+
+constexpr int BLOCK = 256;
+
+__host__ __device__ constexpr int lanes_for(int K, int M) {
+    // the fewest lanes that keep a lane's share of the state at <= 32 floats
+    int L = 1;
+    while (K * M / L > 32 && L < M && L < 64) L *= 2;
+    return L;
+}
+
+__host__ __device__ constexpr int tile_for(int K, int M) {
+    // tokens of s and nu staged per LDS tile: <= 16 KiB of floats, <= 16 tokens
+    int t = 16;
+    while (t > 1 && t * (K + 2) * M * 4 > 16384) t /= 2;
+    return t;
+}
+
+// Memory slot of (lane, v): runs of four consecutive slots per lane (16-byte accesses) when a lane
+// owns a multiple of four slots, lane-interleaved single slots otherwise.
+template <int M, int L>
+__device__ __forceinline__ int slot(int lane, int v) {
+    constexpr int MV = M / L;
+    if constexpr (MV % 4 == 0) return ((v >> 2) * L + lane) * 4 + (v & 3);
+    else return v * L + lane;
+}
+
+template <typename IO, int K>
+__device__ __forceinline__ void load_stage(const LatticeArgs &a, long long row, int c,
+                                           int radius_kind, int rotation_kind,
+                                           float (&rc)[K], float (&rs)[K]) {
+    const IO *alpha = static_cast<const IO *>(a.alpha) + row * a.alpha_row + (long long)c * K;
+    const IO *beta = static_cast<const IO *>(a.beta) + row * a.beta_row + (long long)c * K;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc[k], rs[k]);
+}
+
+// ---------------------------------------------------------------------------------------------
+// summary: Phi and carry of every chunk but the last, from a zero state
+// ---------------------------------------------------------------------------------------------
+template <typename IO, int K, int M>
+__global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
+    constexpr int L = lanes_for(K, M);
+    constexpr int G = BLOCK / L;
+    constexpr int MV = M / L;
+    constexpr int KB = (K + L - 1) / L;          // basis columns of Phi per lane
+    constexpr int TT = tile_for(K, M);
+    const int groups = (a.C + G - 1) / G;
+    const int summarised = a.chunks - 1;
+    int block = blockIdx.x;
+    const int group = block % groups;
+    block /= groups;
+    const int chunk_index = block % summarised;
+    const int b = block / summarised;
+    const int lane = threadIdx.x % L;
+    const int c = group * G + threadIdx.x / L;
+    const bool active = c < a.C;
+    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+
+    __shared__ float s_write[TT * M];
+    float V[K][MV];
+    float P[K][KB];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+        for (int v = 0; v < MV; ++v) V[k][v] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KB; ++i) P[k][i] = (lane + i * L == k) ? 1.0f : 0.0f;
+    }
+    const int first = chunk_index * a.chunk;
+    const int last = min(first + a.chunk, a.T);
+    const IO *write = static_cast<const IO *>(a.write);
+    for (int tile = first; tile < last; tile += TT) {
+        const int n = min(TT, last - tile);
+        __syncthreads();
+        for (int i = threadIdx.x; i < n * M; i += BLOCK)
+            s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
+        __syncthreads();
+        if (!active) continue;
+        for (int tt = 0; tt < n; ++tt) {
+            const long long row = (long long)b * a.T + tile + tt;
+            if (a.valid && !a.valid[row]) continue;
+            float rc[K], rs[K];
+            load_stage<IO, K>(a, row, c, radius_kind, rotation_kind, rc, rs);
+            const float xv = load(static_cast<const IO *>(a.x) + row * a.x_row + c);
+#pragma unroll
+            for (int v = 0; v < MV; ++v) {
+                float U = xv * s_write[tt * M + slot<M, L>(lane, v)];
+#pragma unroll
+                for (int k = K; k >= 1; --k) {
+                    const float delayed = V[k - 1][v];
+                    const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                    if (k < K) V[k][v] = level;
+                }
+                V[0][v] = U;
+            }
+#pragma unroll
+            for (int i = 0; i < KB; ++i) {
+                float U = 0.0f;
+#pragma unroll
+                for (int k = K; k >= 1; --k) {
+                    const float delayed = P[k - 1][i];
+                    const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                    if (k < K) P[k][i] = level;
+                }
+                P[0][i] = U;
+            }
+        }
+    }
+    if (!active) return;
+    const long long plane = ((long long)b * a.chunks + chunk_index) * a.C + c;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+        for (int v = 0; v < MV; ++v) a.carry[(plane * K + k) * M + slot<M, L>(lane, v)] = V[k][v];
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+            const int j = lane + i * L;
+            if (j < K) a.phi[(plane * K + k) * K + j] = P[k][i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// combine: the state entering every chunk, serial over the chunks of one (b, c, m)
+// ---------------------------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(BLOCK) void lattice_combine(LatticeArgs a) {
+    const long long index = (long long)blockIdx.x * BLOCK + threadIdx.x;
+    const long long total = (long long)a.B * a.C * a.M;
+    if (index >= total) return;
+    const int m = index % a.M;
+    const int c = (index / a.M) % a.C;
+    const int b = index / ((long long)a.M * a.C);
+    float S[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        S[k] = a.state_in ? a.state_in[(((long long)b * K + k) * a.C + c) * a.M + m] : 0.0f;
+    for (int j = 0; j < a.chunks; ++j) {
+        const long long plane = ((long long)b * a.chunks + j) * a.C + c;
+        float carry[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float *slot_k = a.carry + (plane * K + k) * a.M + m;
+            carry[k] = (j + 1 < a.chunks) ? *slot_k : 0.0f;
+            *slot_k = S[k];
+        }
+        if (j + 1 == a.chunks) break;
+        const float *phi = a.phi + plane * K * K;
+        float next[K];
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            float value = carry[i];
+#pragma unroll
+            for (int jj = 0; jj < K; ++jj) value = fmaf(phi[i * K + jj], S[jj], value);
+            next[i] = value;
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) S[k] = next[k];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// replay: the scan of one chunk from its entering state, with readout and gate
+// ---------------------------------------------------------------------------------------------
+template <typename IO, int K, int M>
+__global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
+    constexpr int L = lanes_for(K, M);
+    constexpr int G = BLOCK / L;
+    constexpr int MV = M / L;
+    constexpr int TT = tile_for(K, M);
+    const int groups = (a.C + G - 1) / G;
+    int block = blockIdx.x;
+    const int group = block % groups;
+    block /= groups;
+    const int chunk_index = block % a.chunks;
+    const int b = block / a.chunks;
+    const int lane = threadIdx.x % L;
+    const int c = group * G + threadIdx.x / L;
+    const bool active = c < a.C;
+    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+
+    __shared__ float s_write[TT * M];
+    __shared__ float s_read[TT * (K + 1) * M];
+    float V[K][MV];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int v = 0; v < MV; ++v) {
+            float value = 0.0f;
+            if (active) {
+                const int m = slot<M, L>(lane, v);
+                if (chunk_index > 0)
+                    value = a.carry[((((long long)b * a.chunks + chunk_index) * a.C + c) * K + k) * M + m];
+                else if (a.state_in)
+                    value = a.state_in[(((long long)b * K + k) * a.C + c) * M + m];
+            }
+            V[k][v] = value;
+        }
+    const int first = chunk_index * a.chunk;
+    const int last = min(first + a.chunk, a.T);
+    const IO *write = static_cast<const IO *>(a.write);
+    const IO *read = static_cast<const IO *>(a.read);
+    IO *out = static_cast<IO *>(a.out);
+    for (int tile = first; tile < last; tile += TT) {
+        const int n = min(TT, last - tile);
+        __syncthreads();
+        for (int i = threadIdx.x; i < n * M; i += BLOCK)
+            s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
+        for (int i = threadIdx.x; i < n * (K + 1) * M; i += BLOCK) {
+            const int tt = i / ((K + 1) * M), rest = i % ((K + 1) * M);
+            s_read[i] = load(read + ((long long)b * a.T + tile + tt) * a.read_row + rest);
+        }
+        __syncthreads();
+        if (!active) continue;
+        for (int tt = 0; tt < n; ++tt) {
+            const long long row = (long long)b * a.T + tile + tt;
+            if (a.valid && !a.valid[row]) {
+                if (lane == 0) out[row * a.C + c] = from_float<IO>(0.0f);
+                continue;
+            }
+            float rc[K], rs[K], rho[K + 1];
+            load_stage<IO, K>(a, row, c, radius_kind, rotation_kind, rc, rs);
+            const IO *rho_row = static_cast<const IO *>(a.rho) + row * a.rho_row + (long long)c * (K + 1);
+#pragma unroll
+            for (int k = 0; k <= K; ++k) rho[k] = load(rho_row + k);
+            const float xv = load(static_cast<const IO *>(a.x) + row * a.x_row + c);
+            const float gate = silu(load(static_cast<const IO *>(a.gamma) + row * a.gamma_row + c));
+            const float *nu = s_read + tt * (K + 1) * M;
+            float acc[K + 1];
+#pragma unroll
+            for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < MV; ++v) {
+                const int m = slot<M, L>(lane, v);
+                float U = xv * s_write[tt * M + m];
+#pragma unroll
+                for (int k = K; k >= 1; --k) {
+                    const float delayed = V[k - 1][v];
+                    const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                    acc[k] = fmaf(level, nu[k * M + m], acc[k]);
+                    if (k < K) V[k][v] = level;
+                }
+                V[0][v] = U;
+                acc[0] = fmaf(U, nu[m], acc[0]);
+            }
+            float y = 0.0f;
+#pragma unroll
+            for (int k = 0; k <= K; ++k) y = fmaf(rho[k], acc[k], y);
+            y = group_sum<L>(y);
+            if (lane == 0) out[row * a.C + c] = from_float<IO>(gate * y);
+        }
+    }
+    if (active && a.state_out && chunk_index == a.chunks - 1) {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int v = 0; v < MV; ++v)
+                a.state_out[(((long long)b * K + k) * a.C + c) * M + slot<M, L>(lane, v)] = V[k][v];
+    }
+}
+
+template <typename IO, int K, int M>
+int launch_typed(LatticeArgs &a, hipStream_t stream) {
+    constexpr int L = lanes_for(K, M);
+    constexpr int G = BLOCK / L;
+    const long long groups = (a.C + G - 1) / G;
+    if (a.chunks > 1) {
+        const long long blocks = (long long)a.B * (a.chunks - 1) * groups;
+        hipLaunchKernelGGL((lattice_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+        if (int rc = check_launch("lattice_summary")) return rc;
+        const long long threads = (long long)a.B * a.C * M;
+        hipLaunchKernelGGL((lattice_combine<K>), dim3((threads + BLOCK - 1) / BLOCK), dim3(BLOCK),
+                           0, stream, a);
+        if (int rc = check_launch("lattice_combine")) return rc;
+    }
+    const long long blocks = (long long)a.B * a.chunks * groups;
+    hipLaunchKernelGGL((lattice_replay<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+    return check_launch("lattice_replay");
+}
+
+template <typename IO, int K>
+int dispatch_m(LatticeArgs &a, hipStream_t s) {
+    switch (a.M) {
+        case 1: return launch_typed<IO, K, 1>(a, s);
+        case 2: return launch_typed<IO, K, 2>(a, s);
+        case 4: return launch_typed<IO, K, 4>(a, s);
+        case 8: return launch_typed<IO, K, 8>(a, s);
+        case 16: return launch_typed<IO, K, 16>(a, s);
+        case 32: return launch_typed<IO, K, 32>(a, s);
+        case 64: return launch_typed<IO, K, 64>(a, s);
+        case 128: return launch_typed<IO, K, 128>(a, s);
+    }
+    return fail(MIRA_DECLINE, "lattice: unsupported d_m");
+}
+
+template <typename IO>
+int dispatch_k(LatticeArgs &a, hipStream_t s) {
+    switch (a.K) {
+        case 1: return dispatch_m<IO, 1>(a, s);
+        case 2: return dispatch_m<IO, 2>(a, s);
+        case 4: return dispatch_m<IO, 4>(a, s);
+        case 8: return dispatch_m<IO, 8>(a, s);
+    }
+    return fail(MIRA_DECLINE, "lattice: unsupported order K");
+}
+
+}  // namespace
+
+bool lattice_supported(int K, int M, int dtype) {
+    const bool k_ok = K == 1 || K == 2 || K == 4 || K == 8;
+    const bool m_ok = M >= 1 && M <= 128 && (M & (M - 1)) == 0;
+    return k_ok && m_ok && dtype >= MIRA_F32 && dtype <= MIRA_F16;
+}
+
+int lattice_lanes(int K, int M) { return lanes_for(K, M); }
+
+int lattice_plan_chunk(int B, int T, int C, int K, int M) {
+    // Enough (b, chunk, channel-group) blocks to put ~8 on every CU, at >= 16 tokens a chunk.
+    const int G = BLOCK / lanes_for(K, M);
+    const long long base = (long long)B * ((C + G - 1) / G);
+    const long long target = 2048;
+    if (T <= 32 || base >= target) return T;
+    long long chunks = std::min<long long>((target + base - 1) / base, (T + 15) / 16);
+    if (chunks <= 1) return T;
+    int chunk = (int)((T + chunks - 1) / chunks);
+    chunk = (chunk + 15) / 16 * 16;
+    return std::min(chunk, T);
+}
+
+size_t lattice_workspace(int B, int T, int C, int K, int M, int chunk) {
+    if (chunk <= 0 || chunk >= T) return 0;
+    const long long chunks = (T + chunk - 1) / chunk;
+    const long long planes = (long long)B * chunks * C;
+    return (size_t)(planes * K * K + planes * K * M) * sizeof(float);
+}
+
+int lattice_launch(LatticeArgs &a, hipStream_t stream) {
+    switch (a.dtype) {
+        case MIRA_F32: return dispatch_k<float>(a, stream);
+        case MIRA_BF16: return dispatch_k<bf16_t>(a, stream);
+        case MIRA_F16: return dispatch_k<f16_t>(a, stream);
+    }
+    return fail(MIRA_DECLINE, "lattice: unsupported dtype");
+}
+
+}  // namespace mira

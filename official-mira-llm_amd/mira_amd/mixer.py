@@ -1,0 +1,138 @@
+"""MiraMixer on the MI355X plugin: the reference host caller with its constructor and forward
+signature (model/mira_mixer.py:544-856), so model/mira_block.py can use it unchanged.
+
+Parameter layout (model/mira_mixer.py:593-627): input_projection d -> d_e + d_m (no bias),
+to_control d -> d_r, to_gate d -> d_e, coefficient_projection d_r -> alpha | beta | rho | nu
+(d_e K + d_e K + d_e (K+1) + (K+1) d_m), out_proj d_e -> d (no bias). The forward projects,
+splits the fused projections into strided views (no copies, model/mira_mixer.py:807-813), takes
+s = SiLU(raw write), and hands everything to mira_amd.mira.matrix_lattice_iir with the prefix
+cache's state. There is no PyTorch fallback: a declined call raises, as in the reference
+(model/mira_mixer.py:822-824).
+
+The reference's lattice initializer (model/mira_initializer.py, Jeffreys-prior pole placement)
+is out of scope here; parameters use torch's default nn.Linear initialisation.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import mira as plugin
+
+ARCHES = tuple(plugin.ARCH_STAGE)
+
+
+def _declined(signal, order, memory_dimension):
+    batch, tokens, channels = signal.shape
+    ok, detail = plugin.status()
+    return (f"the mira_amd kernel declined [B,T,C]=[{batch},{tokens},{channels}] "
+            f"d_m={memory_dimension} K={order} dtype={signal.dtype}: {detail}. "
+            f"MIRA does not fall back to a PyTorch scan -- build the library with "
+            f"python official-mira-llm_amd/build.py")
+
+
+class MiraMixer(nn.Module):
+    def __init__(self, width, lattice_order=2, d_e=1536, coefficient_bottleneck=48,
+                 memory_dimension=16, dropout=0.0, positive_poles=False,
+                 lattice_initializer="W_uniform_b_jeffreys", lattice_init_horizon=None,
+                 arch="cauchy_x_hyperbolic"):
+        super().__init__()
+        if arch not in ARCHES:
+            raise ValueError(f"arch must be one of {ARCHES}, not {arch!r}")
+        if not 1 <= int(lattice_order) <= 16:
+            raise ValueError("lattice_order must be in [1,16]")
+        self.width = int(width)
+        self.order = self.lattice_order = int(lattice_order)
+        self.inner = int(d_e)
+        self.coefficient_bottleneck = int(coefficient_bottleneck)
+        self.memory_dimension = int(memory_dimension)
+        self.positive_poles = bool(positive_poles)
+        self.arch = arch
+        self.lattice_initializer = lattice_initializer
+        self.lattice_init_horizon = lattice_init_horizon
+        if self.positive_poles and self.order != 1:
+            raise ValueError("positive_poles requires lattice_order=1")
+        if self.positive_poles and self.arch != "cauchy_x_mobius":
+            raise ValueError("positive_poles requires arch='cauchy_x_mobius'")
+        if min(self.inner, self.coefficient_bottleneck, self.memory_dimension) < 1:
+            raise ValueError("d_e, coefficient_bottleneck, and memory_dimension must be positive")
+        channels, order = self.inner, self.order
+        self.input_projection = nn.Linear(self.width, channels + self.memory_dimension, bias=False)
+        self.to_control = nn.Linear(self.width, self.coefficient_bottleneck)
+        self.to_gate = nn.Linear(self.width, channels)
+        alpha_size = beta_size = channels * order
+        rho_size = channels * (order + 1)
+        read_size = (order + 1) * self.memory_dimension
+        self.coefficient_projection = nn.Linear(
+            self.coefficient_bottleneck, alpha_size + beta_size + rho_size + read_size)
+        self.signal_span = (0, channels)
+        self.write_span = (channels, channels + self.memory_dimension)
+        self.alpha_span = (0, alpha_size)
+        self.beta_span = (alpha_size, 2 * alpha_size)
+        self.rho_span = (2 * alpha_size, 2 * alpha_size + rho_size)
+        self.read_span = (2 * alpha_size + rho_size, 2 * alpha_size + rho_size + read_size)
+        self.out_proj = nn.Linear(channels, self.width, bias=False)
+        self.dropout = nn.Dropout(dropout)
+
+    def state_values(self):
+        return self.order * self.inner * self.memory_dimension
+
+    def residual_out(self):
+        return self.out_proj
+
+    def project_recurrence_inputs(self, normalized_x):
+        """(input projection, coefficient projection, gamma) -- one packed GEMM for the three
+        projections of the normalised input (model/mira_mixer.py:657-712)."""
+        projections = (self.input_projection, self.to_gate, self.to_control)
+        weight = torch.cat([p.weight for p in projections])
+        bias = torch.cat([p.bias if p.bias is not None else p.weight.new_zeros(p.out_features)
+                          for p in projections])
+        projected = F.linear(normalized_x, weight, bias)
+        projected_input, gamma, raw_control = projected.split(
+            tuple(p.out_features for p in projections), dim=-1)
+        control = F.silu(raw_control)
+        return projected_input, self.coefficient_projection(control), gamma
+
+    def forward(self, normalized_x, attn_mask=None, cache=None, layer=None):
+        if cache is not None and not (layer is not None and not self.training
+                                      and hasattr(cache, "get")):
+            raise ValueError("streaming cache is not wired into mira-dsp")
+        batch, tokens, _ = normalized_x.shape
+        channels, order, memory = self.inner, self.order, self.memory_dimension
+        alpha_size = channels * order
+        rho_size = channels * (order + 1)
+        read_size = (order + 1) * memory
+        input_projection, coefficients, gamma = self.project_recurrence_inputs(normalized_x)
+        signal, raw_write = input_projection.split((channels, memory), dim=-1)
+        raw_alpha, raw_beta, raw_rho, memory_read = coefficients.split(
+            (alpha_size, alpha_size, rho_size, read_size), dim=-1)
+        if self.positive_poles:
+            value = raw_alpha.float()
+            safe = torch.where(value == 0.0, torch.full_like(value, 1.0e-6), value)
+            raw_alpha = torch.where(value.abs() < 1.0, safe.reciprocal(), value).to(raw_alpha.dtype)
+        memory_write = F.silu(raw_write)
+        raw_alpha = raw_alpha.view(batch, tokens, channels, order)
+        raw_beta = raw_beta.view(batch, tokens, channels, order)
+        raw_rho = raw_rho.view(batch, tokens, channels, order + 1)
+        memory_read = memory_read.view(batch, tokens, order + 1, memory)
+        valid = None if attn_mask is None else attn_mask[:, -tokens:].bool()
+        result = plugin.matrix_lattice_iir(
+            signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
+            raw_beta=raw_beta, valid=valid,
+            state=None if cache is None else cache.get(layer),
+            return_state=cache is not None, arch=self.arch)
+        if result is None:
+            raise RuntimeError(_declined(signal, order, memory))
+        if cache is None:
+            mixed = result
+        else:
+            mixed, final = result
+            cache.put(layer, final)
+            fits, why = cache.within_budget()
+            if not fits:
+                raise ValueError(why)
+        output = self.out_proj(self.dropout(mixed))
+        if valid is not None:
+            output = torch.where(valid.unsqueeze(-1), output, torch.zeros_like(output))
+        return output

@@ -1,0 +1,91 @@
+"""CPU checks of the C-ABI library: it loads without a GPU, exports every entry point that
+include/mira_hip.h declares, and its host-only entry points (planning, workspace sizes, argument
+validation) behave -- no kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from _util import HERE
+
+ROOT = os.path.dirname(HERE)
+HEADER = os.path.join(ROOT, "include", "mira_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mira_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mira_amd import _lib
+
+    library = _lib.library()
+    if library is None:
+        pytest.fail(f"libmira_hip.so does not load: {_lib.why()}")
+    return library
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared()
+    assert len(names) >= 14
+    missing = [name for name in names if not hasattr(lib, name)]
+    assert not missing, f"declared in mira_hip.h but not exported: {missing}"
+
+
+def test_binding_covers_the_header():
+    from mira_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == declared()
+
+
+def test_version_and_support_table(lib):
+    assert b"gfx950" in lib.mira_version()
+    for K in (1, 2, 4, 8):
+        for M in (1, 2, 4, 8, 16, 32, 64, 128):
+            for dtype in (0, 1, 2):
+                assert lib.mira_lattice_supported(K, M, dtype) == 1
+    assert lib.mira_lattice_supported(3, 16, 0) == 0
+    assert lib.mira_lattice_supported(2, 12, 0) == 0
+    assert lib.mira_lattice_supported(2, 16, 3) == 0
+
+
+def test_chunk_plan_and_workspace(lib):
+    # one chunk for short or wide calls: no workspace
+    assert lib.mira_lattice_plan_chunk(1, 16, 256, 2, 16) == 16
+    assert lib.mira_lattice_workspace_bytes(1, 16, 256, 2, 16, 0) == 0
+    chunk = lib.mira_lattice_plan_chunk(1, 8192, 64, 1, 128)
+    assert 16 <= chunk < 8192 and chunk % 16 == 0
+    chunks = -(-8192 // chunk)
+    assert lib.mira_lattice_workspace_bytes(1, 8192, 64, 1, 128, chunk) == \
+        4 * chunks * 64 * (1 + 128)
+    assert lib.mira_diag_workspace_bytes(8, 4096, 2048, 1) > 0
+    assert lib.mira_diag_workspace_bytes(0, 4096, 2048, 1) == 0
+
+
+def test_argument_errors_without_a_launch(lib):
+    """Validation happens before any HIP call: decline (1) or bad argument (2)."""
+    null = None
+    # K = 3 is not built: decline
+    code = lib.mira_lattice_forward(null, 4, null, 12, null, 12, null, 16, null, 4, null, null, 64,
+                                    null, null, null, null, 1, 8, 4, 3, 16, 0, 6, 0, null, 0, null)
+    assert code == 1 and b"K=3" in lib.mira_last_error()
+    # empty batch: bad argument
+    code = lib.mira_lattice_forward(null, 4, null, 8, null, 8, null, 12, null, 4, null, null, 48,
+                                    null, null, null, null, 0, 8, 4, 2, 16, 0, 6, 0, null, 0, null)
+    assert code == 2
+    # unknown arch mode
+    fake = ctypes.c_void_p(16)
+    code = lib.mira_lattice_forward(fake, 4, fake, 8, fake, 8, fake, 12, fake, 4, fake, fake, 48,
+                                    null, null, null, fake, 1, 8, 4, 2, 16, 0, 5, 0, null, 0, null)
+    assert code == 2 and b"arch" in lib.mira_last_error()
+    # diag: width other than 4 declines, D not a multiple of 4 declines
+    assert lib.mira_diag_conv_scan(fake, fake, fake, null, null, null, null, 0, fake, null,
+                                   1, 8, 16, 3, 1, fake, 1 << 20, null) == 1
+    assert lib.mira_diag_conv_scan(fake, fake, fake, null, null, null, null, 0, fake, null,
+                                   1, 8, 6, 4, 1, fake, 1 << 20, null) == 1
+    # gla: d = 64 declines
+    assert lib.mira_gla_step(fake, fake, fake, fake, fake, fake, 1, 1, 64, 64, 1, null) == 1
