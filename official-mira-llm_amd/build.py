@@ -30,9 +30,23 @@ def sources():
     return sorted(os.path.join(CSRC, name) for name in os.listdir(CSRC) if name.endswith(".hip"))
 
 
-def compile_one(source, objdir):
+def source_hash():
+    """sha256 over every csrc file and the public header: compiled into the library and checked
+    by the loader, so a library built from other sources is refused rather than run."""
+    import hashlib
+
+    digest = hashlib.sha256()
+    header = os.path.join(os.path.dirname(HERE), "include", "mira_hip.h")
+    for path in sorted(os.path.join(CSRC, n) for n in os.listdir(CSRC)) + [header]:
+        digest.update(os.path.basename(path).encode())
+        with open(path, "rb") as handle:
+            digest.update(handle.read())
+    return digest.hexdigest()[:16]
+
+
+def compile_one(source, objdir, digest):
     obj = os.path.join(objdir, os.path.basename(source) + ".o")
-    command = [HIPCC, *FLAGS, "-c", source, "-o", obj]
+    command = [HIPCC, *FLAGS, f"-DMIRA_SOURCE_HASH=\"{digest}\"", "-c", source, "-o", obj]
     result = subprocess.run(command, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source}:\n{result.stdout}\n{result.stderr}")
@@ -45,8 +59,9 @@ def build(jobs=None, verbose=True):
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), os.cpu_count() or 1, 8)
+    digest = source_hash()
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objects = list(pool.map(lambda s: compile_one(s, objdir), srcs))
+        objects = list(pool.map(lambda s: compile_one(s, objdir, digest), srcs))
     tmp = LIBRARY + ".tmp"
     command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp]
     result = subprocess.run(command, capture_output=True, text=True)

@@ -34,7 +34,10 @@ extern "C" {
 
 const char *mira_last_error(void) { return g_last_error.c_str(); }
 
-const char *mira_version(void) { return "mira_hip 0.1 gfx950"; }
+#ifndef MIRA_SOURCE_HASH
+#define MIRA_SOURCE_HASH "unknown"
+#endif
+const char *mira_version(void) { return "mira_hip 0.1 gfx950 src:" MIRA_SOURCE_HASH; }
 
 int mira_lattice_supported(int K, int M, int dtype) { return lattice_supported(K, M, dtype) ? 1 : 0; }
 

@@ -94,6 +94,36 @@ __device__ __forceinline__ void store_raw(IO *p, const typename Raw<IO>::type &v
     *reinterpret_cast<typename Raw<IO>::type *>(p) = v;
 }
 
+// PUBLICATION WITHOUT AN L2 WRITE-BACK. A release fence at agent scope writes back the whole L2
+// of the issuing XCD, and a tile publishes twice, so the published records are instead written
+// and read with agent-scope relaxed atomics, which go to the device coherence point instead of
+// the XCD's non-coherent L2; the writer waits for its record stores to complete (vmcnt(0))
+// before it stores the flag, and a reader loads a record only after it has seen the flag.
+__device__ __forceinline__ void publish_value(float *p, float v) {
+    __hip_atomic_store(reinterpret_cast<unsigned *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_pair(float2 *p, float a, float h) {
+    const unsigned long long bits =
+        (unsigned long long)__float_as_uint(a) | ((unsigned long long)__float_as_uint(h) << 32);
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), bits, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float read_value(const float *p) {
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const unsigned *>(p),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ float2 read_pair(const float2 *p) {
+    const unsigned long long bits = __hip_atomic_load(
+        reinterpret_cast<const unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((unsigned)bits), __uint_as_float((unsigned)(bits >> 32)));
+}
+// every store this wave has issued has completed at its coherence point
+__device__ __forceinline__ void stores_complete() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void set_flag(unsigned *flag, unsigned value) {
+    __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Workspace layout (bytes): [0,256) watchdog word | counters[chains] | flags[chains*tiles]
 // | aggregates (A,H)[chains*tiles*TILE_C] | inclusive H[chains*tiles*TILE_C]
 struct Layout {
@@ -292,10 +322,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void di
         // publish the aggregate
         if (tg == 3) {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) agg[slot * TILE_C + cl * VEC + e] = make_float2(At[e], Ht[e]);
+            for (int e = 0; e < VEC; ++e) publish_pair(agg + slot * TILE_C + cl * VEC + e, At[e], Ht[e]);
         }
+        stores_complete();
         if (lane == 48)
-            __hip_atomic_store(flags + slot, tag | 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            set_flag(flags + slot, tag | 1u);
         // look back: token group g inspects predecessor base - g
         float cA[VEC], cH[VEC];
 #pragma unroll
@@ -328,20 +359,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void di
                 __builtin_amdgcn_s_sleep(2);
                 continue;
             }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             float pA[VEC], pH[VEC];
 #pragma unroll
             for (int e = 0; e < VEC; ++e) { pA[e] = 1.0f; pH[e] = 0.0f; }
             if (p >= 0 && tg < first_inclusive) {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
-                    const float2 v = agg[(base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e];
+                    const float2 v = read_pair(agg + (base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e);
                     pA[e] = v.x; pH[e] = v.y;
                 }
             } else if (p >= 0 && tg == first_inclusive) {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e)
-                    pH[e] = inc[(base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e];
+                    pH[e] = read_value(inc + (base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e);
             }
             const int last = first_inclusive < 4 ? first_inclusive : 3;
             for (int g = 0; g <= last; ++g) {
@@ -364,10 +394,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void di
     // publish this tile's inclusive state
     if (tg == 3) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) inc[slot * TILE_C + cl * VEC + e] = fmaf(At[e], hin[e], Ht[e]);
+        for (int e = 0; e < VEC; ++e) publish_value(inc + slot * TILE_C + cl * VEC + e, fmaf(At[e], hin[e], Ht[e]));
     }
-    if (lane == 48)
-        __hip_atomic_store(flags + slot, tag | 2u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    stores_complete();
+    if (lane == 48) set_flag(flags + slot, tag | 2u);
 
     // replay the lane's tokens from its entering state and store y
     float h[VEC];

@@ -66,8 +66,31 @@ def library():
         except (OSError, AttributeError) as error:
             _WHY = f"loading {path} failed: {error}"
             return None
+        expected = _source_hash()
+        built = lib.mira_version().decode().rpartition("src:")[2]
+        if expected is not None and built != expected:
+            _WHY = (f"{path} was built from other sources (src:{built}, tree src:{expected}): "
+                    f"rebuild with `python official-mira-llm_amd/build.py`")
+            return None
         _LIB = lib
         return _LIB
+
+
+def _source_hash():
+    """The build's content hash of csrc/ and include/mira_hip.h (official-mira-llm_amd/build.py),
+    or None when the sources are not beside the library."""
+    import hashlib
+
+    csrc = os.path.join(os.path.dirname(HERE), "csrc")
+    header = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "mira_hip.h")
+    if not (os.path.isdir(csrc) and os.path.exists(header)):
+        return None
+    digest = hashlib.sha256()
+    for path in sorted(os.path.join(csrc, n) for n in os.listdir(csrc)) + [header]:
+        digest.update(os.path.basename(path).encode())
+        with open(path, "rb") as handle:
+            digest.update(handle.read())
+    return digest.hexdigest()[:16]
 
 
 def why():

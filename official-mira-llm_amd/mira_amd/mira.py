@@ -51,9 +51,12 @@ _WORKSPACES = {}
 
 def _row_stride(tensor, tokens):
     """Row stride of a [B,T,C] view with unit channel stride and batch stride T*row, or None
-    (mira.py:315-321)."""
+    (mira.py:315-321). With one token the batch stride is the row stride (torch may give a
+    size-1 axis any stride)."""
     if tensor.stride(2) != 1:
         return None
+    if tokens == 1:
+        return int(tensor.stride(0))
     row = int(tensor.stride(1))
     if int(tensor.stride(0)) != tokens * row:
         return None
@@ -67,6 +70,8 @@ def dense_tail_row_stride(tensor, tokens):
         if int(tensor.stride(axis)) != expected:
             return None
         expected *= int(tensor.shape[axis])
+    if tokens == 1:
+        return int(tensor.stride(0))
     row = int(tensor.stride(1))
     if int(tensor.stride(0)) != tokens * row:
         return None
