@@ -2,63 +2,98 @@
 //
 //     u_t = sum_j w[d,j] x_(t-W+1+j) + bias[d],     h_t = a_t h_(t-1) + (1 - a_t) u_t,     y_t = h_t
 //
-// PREFILL IS ONE PASS OVER HBM. The work is cut into tiles of 64 tokens x TILE_C channels; a tile
-// is one wave (64 lanes = 4 token groups x 16 channel lanes, 16 tokens x VEC channels per lane,
-// VEC = 4 channels = one 8-byte load in bf16). A tile's map h_in -> h_out is affine, (A, H) with
-// A = prod a and H the state reached from zero, so the tiles of one (sequence, channel block) --
-// a chain -- are joined by a decoupled look-back: each tile publishes its aggregate (A, H) as soon
-// as its inputs are in registers, folds its predecessors' aggregates back to the nearest
-// published inclusive state, publishes its own inclusive state, and only then replays its 16
-// tokens per lane from registers and stores y. x and a are read once and y written once:
-// 6 bytes per (b, t, d) in bf16.
+// PREFILL IS ONE PASS OVER HBM. The work is cut into tiles of TILE_T tokens x 256 channels of one
+// sequence; the tiles of one (sequence, channel block) -- a chain -- are joined by a decoupled
+// look-back over their affine maps h_in -> A h_in + H (A = prod a, H the state reached from
+// zero): every tile publishes its aggregate (A, H) as soon as it is known, folds its
+// predecessors' aggregates back to the nearest published inclusive state, and publishes its own
+// inclusive state. x and a are read once and y written once: 6 bytes per (b, t, d) in bf16.
 //
-// Forward progress: a tile index is a ticket drawn from the chain's counter by a running wave,
-// so every tile a wave waits on is held by a wave that is already running (or done); the waits
-// are nevertheless bounded, and a wait that runs out sets the workspace's watchdog word.
-// Counters return to zero at the end of every launch; flags carry a per-launch epoch, so the
-// workspace needs zero-filling only once, when it is allocated.
+// A WORKGROUP IS ONE LOOK-BACK WAVE AND S STREAMING WAVES, persistent over the tiles it draws from
+// its chain's counter. A streaming wave owns TPW consecutive tokens x 256 channels of a tile
+// (64 lanes x 4 channels: one 512-byte row piece per access in bf16) and runs a three-stage
+// pipeline: it issues the loads of tile i+1, computes the map of tile i (keeping b_t = (1-a_t) u_t
+// in LDS), and, after one barrier, replays tile i-1 (h = a h + b) from the entering state the
+// look-back wave resolved meanwhile and stores y.
+// The look-back wave does all the cross-workgroup protocol (publish, poll, fold, publish), so
+// the streaming waves never wait behind its polls: a wave's vector memory operations complete
+// in issue order, and a poll issued by a streaming wave would wait for its own prefetch. The
+// barriers fence only LDS, never outstanding global loads.
+//
+// Forward progress: tickets are drawn in chain order, a look-back wave resolves its tiles in
+// ticket order, and a tile only waits on lower tickets, so the lowest unresolved tile always
+// progresses; the waits are nevertheless bounded, and a wait that runs out sets the workspace's
+// watchdog word. Counters return to zero at the end of every launch; flags carry a per-launch
+// epoch, so the workspace needs zero-filling only once, when it is allocated.
 #include "mira_device.hpp"
 #include "mira_abi_internal.hpp"
 
+#include <algorithm>
 #include <atomic>
 
 namespace mira {
 namespace {
 
-constexpr int CL = 16;            // channel lanes per wave
-constexpr int TG = 4;             // token groups per wave
-// tokens per lane: 16 of a 16-bit type (8-byte packs), 8 of float32 (16-byte packs), so a lane
-// holds 32 registers of x and 32 of a either way
-__host__ __device__ constexpr int tokens_per_lane(int element_bytes) { return element_bytes == 4 ? 8 : 16; }
-constexpr unsigned SPIN_LIMIT = 1u << 22;
+constexpr int VEC = 4;            // channels per lane
+constexpr int STREAMS = 7;        // streaming waves per workgroup (plus one look-back wave)
+constexpr int TILE_C = 64 * VEC;  // channels per tile
+constexpr int WINDOW = 4;         // predecessors the look-back inspects per round
+constexpr unsigned SPIN_LIMIT = 1u << 20;
+constexpr unsigned OUT_OF_RANGE = 0x80000000u;   // a buffer offset past every record
+constexpr int NT = 2;             // non-temporal cache policy for the a stream and y
 
-// Four channels per lane: one 8-byte load of a 16-bit type, one 16-byte load of float32.
-constexpr int VEC = 4;
-template <typename IO> struct Raw { typedef uint2 type; };
-template <> struct Raw<float> { typedef uint4 type; };
+// tokens per streaming wave and tile: 8 of a 16-bit type (8-byte packs), 4 of float32 (16-byte
+// packs), so a lane holds 16 registers of x and 16 of a per tile either way
+__host__ __device__ constexpr int tokens_per_wave(int element_bytes) {
+    return element_bytes == 4 ? 4 : 8;
+}
 
-template <typename IO>
-__device__ __forceinline__ typename Raw<IO>::type raw_zero() {
-    typename Raw<IO>::type r;
-    __builtin_memset(&r, 0, sizeof(r));
-    return r;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <typename IO> struct Raw { typedef u32x2 type; };
+template <> struct Raw<float> { typedef u32x4 type; };
+
+// a buffer resource over one sequence's [T, D] rows (raw addressing, 32-bit offsets)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t resource(const void *base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+template <typename IO, int POLICY = 0>
+__device__ __forceinline__ typename Raw<IO>::type load_pack(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    if constexpr (sizeof(IO) == 4) return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY);
+    else return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POLICY);
+}
+
+template <typename IO, int POLICY = 0>
+__device__ __forceinline__ void store_pack(__amdgpu_buffer_rsrc_t r, unsigned off,
+                                           const typename Raw<IO>::type &v) {
+    if constexpr (sizeof(IO) == 4) __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, POLICY);
+    else __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, POLICY);
+}
+
+__device__ __forceinline__ float low_half(unsigned w, bf16_t) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float high_half(unsigned w, bf16_t) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float low_half(unsigned w, f16_t) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+}
+__device__ __forceinline__ float high_half(unsigned w, f16_t) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
 }
 
 template <typename IO>
 __device__ __forceinline__ void unpack(const typename Raw<IO>::type &p, float (&f)[VEC]) {
     if constexpr (sizeof(IO) == 4) {
-        f[0] = __uint_as_float(p.x); f[1] = __uint_as_float(p.y);
-        f[2] = __uint_as_float(p.z); f[3] = __uint_as_float(p.w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(p[i]);
     } else {
-        const uint32_t words[2] = {p.x, p.y};
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const uint16_t lo = words[i] & 0xffffu, hi = words[i] >> 16;
-            IO l, h;
-            __builtin_memcpy(&l, &lo, 2);
-            __builtin_memcpy(&h, &hi, 2);
-            f[2 * i] = to_float(l);
-            f[2 * i + 1] = to_float(h);
+            f[2 * i] = low_half(p[i], IO{});
+            f[2 * i + 1] = high_half(p[i], IO{});
         }
     }
 }
@@ -67,31 +102,22 @@ template <typename IO>
 __device__ __forceinline__ typename Raw<IO>::type pack(const float (&f)[VEC]) {
     typename Raw<IO>::type p;
     if constexpr (sizeof(IO) == 4) {
-        p.x = __float_as_uint(f[0]); p.y = __float_as_uint(f[1]);
-        p.z = __float_as_uint(f[2]); p.w = __float_as_uint(f[3]);
-    } else {
-        uint32_t words[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = __float_as_uint(f[i]);
+    } else if constexpr (__is_same(IO, bf16_t)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const IO l = from_float<IO>(f[2 * i]), h = from_float<IO>(f[2 * i + 1]);
-            uint16_t lo, hi;
-            __builtin_memcpy(&lo, &l, 2);
-            __builtin_memcpy(&hi, &h, 2);
-            words[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+            const f32x2 v = {f[2 * i], f[2 * i + 1]};
+            p[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
         }
-        p.x = words[0]; p.y = words[1];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const f32x2 v = {f[2 * i], f[2 * i + 1]};
+            p[i] = __builtin_bit_cast(unsigned, __builtin_convertvector(v, f16x2));
+        }
     }
     return p;
-}
-
-template <typename IO>
-__device__ __forceinline__ typename Raw<IO>::type load_raw(const IO *p) {
-    return *reinterpret_cast<const typename Raw<IO>::type *>(p);
-}
-
-template <typename IO>
-__device__ __forceinline__ void store_raw(IO *p, const typename Raw<IO>::type &v) {
-    *reinterpret_cast<typename Raw<IO>::type *>(p) = v;
 }
 
 // PUBLICATION WITHOUT AN L2 WRITE-BACK. A release fence at agent scope writes back the whole L2
@@ -131,12 +157,12 @@ struct Layout {
     size_t counters, flags, agg, inc, total;
 };
 
-__host__ __device__ inline Layout layout(int B, int T, int D, int vec, int element_bytes) {
-    const int TILE_T = TG * tokens_per_lane(element_bytes);
+__host__ __device__ inline Layout layout(int B, int T, int D, int element_bytes) {
     Layout l;
-    l.tile_c = (long long)CL * vec;
+    const int tile_t = STREAMS * tokens_per_wave(element_bytes);
+    l.tile_c = TILE_C;
     l.chains = (long long)B * ((D + l.tile_c - 1) / l.tile_c);
-    l.tiles = (T + TILE_T - 1) / TILE_T;
+    l.tiles = (T + tile_t - 1) / tile_t;
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     l.counters = 256;
     l.flags = l.counters + up(l.chains * 4);
@@ -146,39 +172,170 @@ __host__ __device__ inline Layout layout(int B, int T, int D, int vec, int eleme
     return l;
 }
 
+// LDS-only fences around a barrier: they order LDS accesses and wait for nothing else, so a
+// wave's outstanding global loads stay in flight across the barrier
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename IO, int W>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void diag_scan_kernel(DiagArgs a, unsigned char *ws,
-                                                       unsigned epoch) {
-    constexpr int TILE_C = CL * VEC;
+__global__ __launch_bounds__((STREAMS + 1) * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_per_chain) {
+    constexpr int TPW = tokens_per_wave(sizeof(IO));
+    constexpr int TILE_T = STREAMS * TPW;
     constexpr int H = W - 1;                         // conv history
     typedef typename Raw<IO>::type RawT;
-    constexpr int TPT = tokens_per_lane(sizeof(IO));
-    constexpr int TILE_T = TG * TPT;
-    const Layout lay = layout(a.B, a.T, a.D, VEC, sizeof(IO));
+    const Layout lay = layout(a.B, a.T, a.D, sizeof(IO));
     unsigned *watchdog = reinterpret_cast<unsigned *>(ws);
     unsigned *counters = reinterpret_cast<unsigned *>(ws + lay.counters);
     unsigned *flags = reinterpret_cast<unsigned *>(ws + lay.flags);
     float2 *agg = reinterpret_cast<float2 *>(ws + lay.agg);
     float *inc = reinterpret_cast<float *>(ws + lay.inc);
 
-    const int lane = threadIdx.x;
-    const int tg = lane >> 4, cl = lane & 15;
+    __shared__ int s_ticket[4];                      // tickets t_i, ring of four
+    __shared__ float2 s_map[3][STREAMS][VEC][64];    // streaming waves' maps, by i mod 3
+    __shared__ float s_hin[2][VEC][64];              // resolved entering state, by tile parity
+    __shared__ float4 s_b[2][STREAMS][TPW][64];      // b_t = (1 - a_t) u_t of a wave's tokens
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int chain = blockIdx.x % lay.chains;
-    unsigned ticket = 0;
-    if (lane == 0) {
-        ticket = atomicAdd(counters + chain, 1u);
-        if (ticket == lay.tiles - 1)                 // every ticket of this chain is drawn
-            __hip_atomic_store(counters + chain, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const int tile = __shfl(ticket, 0);
     const int cblocks = (a.D + TILE_C - 1) / TILE_C;
     const int b = chain / cblocks;
-    const int d0 = (chain % cblocks) * TILE_C + cl * VEC;
+    const int d0 = (chain % cblocks) * TILE_C + lane * VEC;
     const bool dact = d0 < a.D;
-    const int t0 = tile * TILE_T + tg * TPT;
     const long long row0 = (long long)b * a.T;
+    const unsigned tag = (epoch & 0x3fffffffu) << 2;
+    const unsigned last_draw = (unsigned)lay.tiles + 3u * (unsigned)groups_per_chain - 1u;
 
-    // per-channel conv weights
+    if (wave == 0) {
+        // ------------------------------------------------------------------ the look-back wave
+        // Tickets are drawn three tiles ahead (a streaming wave reads t_(i+1) before barrier
+        // X_i, and the look-back wave writes it between X_(i-2) and X_(i-1)). Each workgroup
+        // therefore draws exactly three tickets past the last tile, so the counter's last draw
+        // is tiles + 3 groups - 1 and the workgroup that draws it resets the counter.
+        auto draw = [&]() -> int {
+            unsigned ticket = 0;
+            if (lane == 0) {
+                ticket = atomicAdd(counters + chain, 1u);
+                if (ticket == last_draw)
+                    __hip_atomic_store(counters + chain, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return (int)__shfl(ticket, 0);
+        };
+        const int t0 = draw(), t1 = draw(), t2 = draw();
+        if (lane == 0) { s_ticket[0] = t0; s_ticket[1] = t1; s_ticket[2] = t2; }
+        lds_barrier();                                               // P
+        for (int i = 0;; ++i) {
+            const int tile = s_ticket[i & 3];
+            lds_barrier();                                           // X_i: maps of tile i
+            if (tile >= lay.tiles) break;
+            // the tile's map: the streaming waves' maps in token order
+            float At[VEC], Ht[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) { At[e] = 1.0f; Ht[e] = 0.0f; }
+            for (int g = 0; g < STREAMS; ++g) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const float2 m = s_map[i % 3][g][e][lane];
+                    Ht[e] = fmaf(m.x, Ht[e], m.y);
+                    At[e] *= m.x;
+                }
+            }
+            const long long slot = (long long)chain * lay.tiles + tile;
+            float hin[VEC];
+            if (tile == 0) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e)
+                    hin[e] = (dact && a.h0) ? a.h0[(long long)b * a.D + d0 + e] : 0.0f;
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) publish_pair(agg + slot * TILE_C + lane * VEC + e, At[e], Ht[e]);
+                stores_complete();
+                if (lane == 0) set_flag(flags + slot, tag | 1u);
+                // look back, WINDOW predecessors per round: lane j < WINDOW polls base - j
+                float cA[VEC], cH[VEC];
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) { cA[e] = 1.0f; cH[e] = 0.0f; hin[e] = 0.0f; }
+                long long base = tile - 1;
+                unsigned spins = 0;
+                while (true) {
+                    unsigned status = 2;                             // before the first tile
+                    if (lane < WINDOW && base - lane >= 0) {
+                        const unsigned f = __hip_atomic_load(flags + (long long)chain * lay.tiles + base - lane,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        status = (f & ~3u) == tag ? (f & 3u) : 0u;
+                    }
+                    const unsigned long long ready = __ballot(lane < WINDOW && status >= 1);
+                    const unsigned long long inclusive = __ballot(lane < WINDOW && status == 2);
+                    const int first_inclusive = inclusive ? __builtin_ctzll(inclusive) : WINDOW;
+                    const unsigned long long need = (1ull << first_inclusive) - 1ull;
+                    if ((ready & need) != need) {
+                        if (++spins > SPIN_LIMIT) {
+                            if (lane == 0)
+                                __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        continue;
+                    }
+                    // the records, nearest first: aggregates, then the inclusive state
+                    const int count = first_inclusive < WINDOW ? first_inclusive + 1 : WINDOW;
+                    float2 rec[WINDOW][VEC];
+#pragma unroll
+                    for (int g = 0; g < WINDOW; ++g) {
+                        if (g < count) {
+                            const long long record = ((long long)chain * lay.tiles + base - g) * TILE_C + lane * VEC;
+#pragma unroll
+                            for (int e = 0; e < VEC; ++e)
+                                rec[g][e] = g < first_inclusive ? read_pair(agg + record + e)
+                                                                : make_float2(0.0f, read_value(inc + record + e));
+                        }
+                    }
+#pragma unroll
+                    for (int g = 0; g < WINDOW; ++g) {
+                        if (g < count) {
+#pragma unroll
+                            for (int e = 0; e < VEC; ++e) {
+                                if (g < first_inclusive) {           // fold one more aggregate
+                                    cH[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
+                                    cA[e] *= rec[g][e].x;
+                                } else {                             // the inclusive state
+                                    hin[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
+                                }
+                            }
+                        }
+                    }
+                    if (first_inclusive < WINDOW) break;
+                    base -= WINDOW;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                publish_value(inc + slot * TILE_C + lane * VEC + e, fmaf(At[e], hin[e], Ht[e]));
+                s_hin[i & 1][e][lane] = hin[e];
+            }
+            stores_complete();
+            if (lane == 0) set_flag(flags + slot, tag | 2u);
+            const int t3 = draw();
+            if (lane == 0) s_ticket[(i + 3) & 3] = t3;
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------------- a streaming wave
+    const int sw = wave - 1;                                         // token group of the tile
+    const unsigned seq_bytes = (unsigned)a.T * (unsigned)a.D * (unsigned)sizeof(IO);
+    const IO *x = static_cast<const IO *>(a.x);
+    const __amdgpu_buffer_rsrc_t xr = resource(x + row0 * a.D, seq_bytes);
+    const __amdgpu_buffer_rsrc_t ar = resource(static_cast<const IO *>(a.a) + row0 * a.D, seq_bytes);
+    const __amdgpu_buffer_rsrc_t yr = resource(static_cast<IO *>(a.y) + row0 * a.D, seq_bytes);
+    auto offset = [&](int t) -> unsigned {
+        return (dact && t >= 0 && t < a.T)
+                   ? ((unsigned)t * (unsigned)a.D + (unsigned)d0) * (unsigned)sizeof(IO)
+                   : OUT_OF_RANGE;
+    };
     float wv[VEC][W], bias[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -186,276 +343,142 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void di
         for (int j = 0; j < W; ++j) wv[e][j] = dact ? a.w[(long long)(d0 + e) * W + j] : 0.0f;
         bias[e] = (dact && a.bias) ? a.bias[d0 + e] : 0.0f;
     }
-
-    // this lane's 16 tokens of x and a, as raw packs
-    RawT xp[TPT], ap[TPT];
-    const IO *x = static_cast<const IO *>(a.x);
-    const IO *av = static_cast<const IO *>(a.a);
-    // a wave-uniform base per sequence and a 32-bit byte offset per lane (T * D elements of one
-    // sequence fit in 4 GiB, checked by the host), so each access needs one offset register
-    const char *xs = reinterpret_cast<const char *>(x + row0 * a.D);
-    const char *as = reinterpret_cast<const char *>(av + row0 * a.D);
-    const uint32_t lane_off = ((uint32_t)t0 * (uint32_t)a.D + (uint32_t)d0) * (uint32_t)sizeof(IO);
-    const uint32_t row_bytes = (uint32_t)a.D * (uint32_t)sizeof(IO);
+    // the H x tokens before token t (the conv history), as raw packs of x; before the first
+    // token of this call they come from the ring, or are zero
+    auto history = [&](int t, RawT (&hist)[H]) {
 #pragma unroll
-    for (int i = 0; i < TPT; ++i) {
-        const int t = t0 + i;
-        if (dact && t < a.T) {
-            xp[i] = *reinterpret_cast<const RawT *>(xs + (lane_off + i * row_bytes));
-            ap[i] = *reinterpret_cast<const RawT *>(as + (lane_off + i * row_bytes));
-        } else {
-            xp[i] = raw_zero<IO>();
-            ap[i] = raw_zero<IO>();
-        }
-    }
-
-    // conv history: the H tokens before t0, from the previous token group's registers, or (first
-    // group) from HBM, the ring, or zero
-    float hist[H][VEC];
+        for (int j = 0; j < H; ++j) {
+            const int tt = t - H + j;
+            if (tt >= 0 || !a.ring_in) {
+                hist[j] = load_pack<IO>(xr, offset(tt));
+            } else {
+                float f[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
+                const long long stream = a.pos + tt;
+                if (dact && stream >= 0) {
+                    const IO *ring = static_cast<const IO *>(a.ring_in);
+                    const int s = (int)(stream % H);
 #pragma unroll
-    for (int j = 0; j < H; ++j) {
-        RawT p;
-        uint32_t *pw = reinterpret_cast<uint32_t *>(&p);
-        const uint32_t *sw = reinterpret_cast<const uint32_t *>(&xp[TPT - H + j]);
-#pragma unroll
-        for (int word = 0; word < (int)(sizeof(RawT) / 4); ++word)
-            pw[word] = __shfl(sw[word], (lane - 16) & 63);
-        float f[VEC];
-        unpack<IO>(p, f);
-        if (tg == 0) {
-            const int t = t0 - H + j;                  // token index local to this call
-            const long long stream = a.pos + t;        // index in the whole stream
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) f[e] = 0.0f;
-            if (dact && t >= 0) {
-                unpack<IO>(load_raw(x + (row0 + t) * a.D + d0), f);
-            } else if (dact && stream >= 0 && a.ring_in) {
-                const IO *ring = static_cast<const IO *>(a.ring_in);
-                const int s = (int)(stream % H);
-#pragma unroll
-                for (int e = 0; e < VEC; ++e)
-                    f[e] = load(ring + ((long long)b * a.D + d0 + e) * H + s);
+                    for (int e = 0; e < VEC; ++e) f[e] = load(ring + ((long long)b * a.D + d0 + e) * H + s);
+                }
+                hist[j] = pack<IO>(f);
             }
         }
+    };
+    auto fetch = [&](int tile, RawT (&xp)[TPW], RawT (&ap)[TPW], RawT (&hist)[H]) {
+        const int t0 = tile * TILE_T + sw * TPW;
+        const bool live = tile < lay.tiles;
+        if (live) history(t0, hist);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) hist[j][e] = f[e];
-    }
-
-    // local scan from zero: the lane's map (A, H) over its tokens
-    float A[VEC], Hs[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) { A[e] = 1.0f; Hs[e] = 0.0f; }
-    {
+        for (int k = 0; k < TPW; ++k) {
+            const unsigned off = live ? offset(t0 + k) : OUT_OF_RANGE;
+            xp[k] = load_pack<IO>(xr, off);
+            ap[k] = load_pack<IO, NT>(ar, off);
+        }
+    };
+    // first pass: conv and decay over the wave's tokens from zero, giving the wave's map (A, H)
+    // and b_t = (1 - a_t) u_t, which goes to LDS for the replay
+    auto summarise = [&](const RawT (&xp)[TPW], const RawT (&ap)[TPW], const RawT (&hist)[H],
+                         float4 (&bout)[TPW][64], float (&A)[VEC], float (&h)[VEC]) {
         float win[H][VEC];
 #pragma unroll
-        for (int j = 0; j < H; ++j)
+        for (int j = 0; j < H; ++j) unpack<IO>(hist[j], win[j]);
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) win[j][e] = hist[j][e];
-#pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            float xf[VEC], af[VEC];
-            unpack<IO>(xp[i], xf);
-            unpack<IO>(ap[i], af);
-            const bool live = t0 + i < a.T;
+        for (int k = 0; k < TPW; ++k) {
+            float xf[VEC], af[VEC], bv[VEC];
+            unpack<IO>(xp[k], xf);
+            unpack<IO>(ap[k], af);
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
                 float u = bias[e];
 #pragma unroll
                 for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], win[j][e], u);
                 u = fmaf(wv[e][H], xf[e], u);
-                if (live) {
-                    Hs[e] = fmaf(af[e], Hs[e], (1.0f - af[e]) * u);
-                    A[e] *= af[e];
-                }
+                bv[e] = fmaf(-af[e], u, u);
+                h[e] = fmaf(af[e], h[e], bv[e]);
+                A[e] *= af[e];
 #pragma unroll
                 for (int j = 0; j + 1 < H; ++j) win[j][e] = win[j + 1][e];
                 win[H - 1][e] = xf[e];
             }
+            bout[k][lane] = make_float4(bv[0], bv[1], bv[2], bv[3]);
         }
-    }
-
-    // The replay below recomputes the conv and unpacks x and a again from the raw packs rather
-    // than keeping 2 x 16 x VEC floats alive across the look-back: hide the packs' values from
-    // the optimiser so that it cannot reuse the first pass's results.
+    };
+    // replay: h = a h + b from the wave's entering state, storing y
+    auto replay = [&](int t0, const RawT (&ap)[TPW], const float4 (&bin)[TPW][64], float (&h)[VEC]) {
 #pragma unroll
-    for (int i = 0; i < TPT; ++i) {
-        uint32_t *xw = reinterpret_cast<uint32_t *>(&xp[i]);
-        uint32_t *aw = reinterpret_cast<uint32_t *>(&ap[i]);
-#pragma unroll
-        for (int word = 0; word < (int)(sizeof(RawT) / 4); ++word) {
-            asm volatile("" : "+v"(xw[word]));
-            asm volatile("" : "+v"(aw[word]));
-        }
-    }
-
-    // inclusive scan of the four token groups' maps (later o earlier = (A_l A_e, A_l H_e + H_l))
-#pragma unroll
-    for (int offset = 16; offset < 64; offset <<= 1) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            const float pa = __shfl_up(A[e], offset, 64);
-            const float ph = __shfl_up(Hs[e], offset, 64);
-            if (lane >= offset) {
-                Hs[e] = fmaf(A[e], ph, Hs[e]);
-                A[e] *= pa;
-            }
-        }
-    }
-    float Ae[VEC], He[VEC], At[VEC], Ht[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-        const float pa = __shfl_up(A[e], 16, 64), ph = __shfl_up(Hs[e], 16, 64);
-        Ae[e] = tg == 0 ? 1.0f : pa;                    // this group's exclusive in-tile map
-        He[e] = tg == 0 ? 0.0f : ph;
-        At[e] = __shfl(A[e], 48 + cl, 64);              // the whole tile's map
-        Ht[e] = __shfl(Hs[e], 48 + cl, 64);
-    }
-
-    const long long slot = (long long)chain * lay.tiles + tile;
-    const unsigned tag = (epoch & 0x3fffffffu) << 2;
-    float hin[VEC];
-    if (tile == 0) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e)
-            hin[e] = (dact && a.h0) ? a.h0[(long long)b * a.D + d0 + e] : 0.0f;
-    } else {
-        // publish the aggregate
-        if (tg == 3) {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) publish_pair(agg + slot * TILE_C + cl * VEC + e, At[e], Ht[e]);
-        }
-        stores_complete();
-        if (lane == 48)
-            set_flag(flags + slot, tag | 1u);
-        // look back: token group g inspects predecessor base - g
-        float cA[VEC], cH[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) { cA[e] = 1.0f; cH[e] = 0.0f; hin[e] = 0.0f; }
-        long long base = tile - 1;
-        unsigned spins = 0;
-        while (true) {
-            const long long p = base - tg;
-            unsigned status = 2;
-            if (p >= 0) {
-                const unsigned f = __hip_atomic_load(flags + (long long)chain * lay.tiles + p,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                status = (f & ~3u) == tag ? (f & 3u) : 0u;
-            }
-            const unsigned long long ready = __ballot(status >= 1 && cl == 0);
-            const unsigned long long inclusive = __ballot(status == 2 && cl == 0);
-            int first_inclusive = 4;
-#pragma unroll
-            for (int g = 3; g >= 0; --g)
-                if ((inclusive >> (16 * g)) & 1ull) first_inclusive = g;
-            bool all_ready = true;
-            for (int g = 0; g < first_inclusive; ++g)
-                if (!((ready >> (16 * g)) & 1ull)) all_ready = false;
-            if (!all_ready) {
-                if (++spins > SPIN_LIMIT) {
-                    if (lane == 0)
-                        __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-                continue;
-            }
-            float pA[VEC], pH[VEC];
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) { pA[e] = 1.0f; pH[e] = 0.0f; }
-            if (p >= 0 && tg < first_inclusive) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float2 v = read_pair(agg + (base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e);
-                    pA[e] = v.x; pH[e] = v.y;
-                }
-            } else if (p >= 0 && tg == first_inclusive) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e)
-                    pH[e] = read_value(inc + (base - tg + (long long)chain * lay.tiles) * TILE_C + cl * VEC + e);
-            }
-            const int last = first_inclusive < 4 ? first_inclusive : 3;
-            for (int g = 0; g <= last; ++g) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float ga = __shfl(pA[e], 16 * g + cl, 64);
-                    const float gh = __shfl(pH[e], 16 * g + cl, 64);
-                    if (g < first_inclusive) {         // fold one more aggregate: c o F_p
-                        cH[e] = fmaf(cA[e], gh, cH[e]);
-                        cA[e] *= ga;
-                    } else {                           // the inclusive state ends the walk
-                        hin[e] = fmaf(cA[e], gh, cH[e]);
-                    }
-                }
-            }
-            if (first_inclusive < 4) break;
-            base -= 4;
-        }
-    }
-    // publish this tile's inclusive state
-    if (tg == 3) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) publish_value(inc + slot * TILE_C + cl * VEC + e, fmaf(At[e], hin[e], Ht[e]));
-    }
-    stores_complete();
-    if (lane == 48) set_flag(flags + slot, tag | 2u);
-
-    // replay the lane's tokens from its entering state and store y
-    float h[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) h[e] = fmaf(Ae[e], hin[e], He[e]);
-    IO *y = static_cast<IO *>(a.y);
-    char *ys = reinterpret_cast<char *>(y + row0 * a.D);
-    {
-        float win[H][VEC];
-#pragma unroll
-        for (int j = 0; j < H; ++j)
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) win[j][e] = hist[j][e];
-#pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            float xf[VEC], af[VEC], out[VEC];
-            unpack<IO>(xp[i], xf);
-            unpack<IO>(ap[i], af);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                float u = bias[e];
-#pragma unroll
-                for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], win[j][e], u);
-                u = fmaf(wv[e][H], xf[e], u);
-                h[e] = fmaf(af[e], h[e], (1.0f - af[e]) * u);
-                out[e] = h[e];
-#pragma unroll
-                for (int j = 0; j + 1 < H; ++j) win[j][e] = win[j + 1][e];
-                win[H - 1][e] = xf[e];
-            }
-            const int t = t0 + i;
-            if (dact && t < a.T)
-                *reinterpret_cast<RawT *>(ys + (lane_off + i * row_bytes)) = pack<IO>(out);
-            if (dact && t == a.T - 1 && a.hT) {
+        for (int k = 0; k < TPW; ++k) {
+            float af[VEC];
+            unpack<IO>(ap[k], af);
+            const float4 bq = bin[k][lane];
+            h[0] = fmaf(af[0], h[0], bq.x);
+            h[1] = fmaf(af[1], h[1], bq.y);
+            h[2] = fmaf(af[2], h[2], bq.z);
+            h[3] = fmaf(af[3], h[3], bq.w);
+            store_pack<IO, NT>(yr, offset(t0 + k), pack<IO>(h));
+            if (dact && t0 + k == a.T - 1 && a.hT) {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) a.hT[(long long)b * a.D + d0 + e] = h[e];
             }
         }
-    }
+    };
 
-    // the ring after this call: the last H stream tokens, each in slot (stream index mod H)
-    if (a.ring_out && tile == lay.tiles - 1 && tg == 0 && dact) {
-        const IO *ring_in = static_cast<const IO *>(a.ring_in);
-        IO *ring_out = static_cast<IO *>(a.ring_out);
+    lds_barrier();                                                   // P
+    int tile_prev = lay.tiles, tile_cur = s_ticket[0];
+    RawT xc[TPW], ac[TPW], hc[H];                                    // tile i (map pending)
+    RawT aq[TPW];                                                    // tile i - 1 (replay pending)
+    fetch(tile_cur, xc, ac, hc);
+    for (int i = 0;; ++i) {
+        const int tile_next = s_ticket[(i + 1) & 3];
+        RawT xn[TPW], an[TPW], hn[H];                                // tile i + 1 (loads in flight)
+        fetch(tile_next, xn, an, hn);
+        if (tile_cur < lay.tiles) {
+            float A[VEC] = {1.0f, 1.0f, 1.0f, 1.0f}, Hs[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
+            summarise(xc, ac, hc, s_b[i & 1][sw], A, Hs);
 #pragma unroll
-        for (int j = 0; j < H; ++j) {
-            const long long stream = a.pos + a.T - H + j;   // one of the last H stream tokens
-            const long long t = a.T - H + j;                // its index in this call
-            const int s = (int)(((stream % H) + H) % H);
+            for (int e = 0; e < VEC; ++e) s_map[i % 3][sw][e][lane] = make_float2(A[e], Hs[e]);
+        }
+        lds_barrier();                                               // X_i
+        if (tile_prev < lay.tiles) {
+            // entering state of this wave in tile i - 1: the tile's resolved state carried
+            // through the maps of the streaming waves before this one
+            float h[VEC];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const long long at = ((long long)b * a.D + d0 + e) * H + s;
-                if (stream < 0) ring_out[at] = from_float<IO>(0.0f);
-                else if (t >= 0) ring_out[at] = x[(row0 + t) * a.D + d0 + e];
-                else if (!ring_in) ring_out[at] = from_float<IO>(0.0f);
-                else if (ring_in != ring_out) ring_out[at] = ring_in[at];
+            for (int e = 0; e < VEC; ++e) h[e] = s_hin[(i - 1) & 1][e][lane];
+            for (int g = 0; g < sw; ++g) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const float2 m = s_map[(i + 2) % 3][g][e][lane];       // tile i - 1
+                    h[e] = fmaf(m.x, h[e], m.y);
+                }
+            }
+            replay(tile_prev * TILE_T + sw * TPW, aq, s_b[(i - 1) & 1][sw], h);
+            // the ring after this call: the last H stream tokens, each in slot (stream mod H)
+            if (a.ring_out && tile_prev == lay.tiles - 1 && sw == 0 && dact) {
+                const IO *ring_in = static_cast<const IO *>(a.ring_in);
+                IO *ring_out = static_cast<IO *>(a.ring_out);
+#pragma unroll
+                for (int j = 0; j < H; ++j) {
+                    const long long stream = a.pos + a.T - H + j;
+                    const long long t = a.T - H + j;
+                    const int s = (int)(((stream % H) + H) % H);
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) {
+                        const long long at = ((long long)b * a.D + d0 + e) * H + s;
+                        if (stream < 0) ring_out[at] = from_float<IO>(0.0f);
+                        else if (t >= 0) ring_out[at] = x[(row0 + t) * a.D + d0 + e];
+                        else if (!ring_in) ring_out[at] = from_float<IO>(0.0f);
+                        else if (ring_in != ring_out) ring_out[at] = ring_in[at];
+                    }
+                }
             }
         }
+        if (tile_cur >= lay.tiles) break;
+        tile_prev = tile_cur;
+        tile_cur = tile_next;
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) { aq[k] = ac[k]; xc[k] = xn[k]; ac[k] = an[k]; }
+#pragma unroll
+        for (int j = 0; j < H; ++j) hc[j] = hn[j];
     }
 }
 
@@ -463,18 +486,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void di
 template <typename IO, int W>
 __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstate) {
     constexpr int H = W - 1;
+    typedef typename Raw<IO>::type RawT;
     const long long index = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long per_row = a.D / VEC;
     if (index >= (long long)a.B * per_row) return;
     const int b = index / per_row;
     const int d0 = (index % per_row) * VEC;
     const IO *x = static_cast<const IO *>(a.x);
-    const IO *av = static_cast<const IO *>(a.a);
     IO *ring = static_cast<IO *>(a.ring_out);
     const long long at = (long long)b * a.D + d0;
-    float xf[VEC], af[VEC], h[VEC], out[VEC];
-    unpack<IO>(load_raw(x + at), xf);
-    unpack<IO>(load_raw(av + at), af);
+    float xf[VEC], af[VEC], h[VEC];
+    unpack<IO>(*reinterpret_cast<const RawT *>(x + at), xf);
+    unpack<IO>(*reinterpret_cast<const RawT *>(static_cast<const IO *>(a.a) + at), af);
     {
         const float4 v = *reinterpret_cast<const float4 *>(hstate + at);
         h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
@@ -493,24 +516,44 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
         }
         u = fmaf(a.w[d * W + H], xf[e], u);
         h[e] = fmaf(af[e], h[e], (1.0f - af[e]) * u);
-        out[e] = h[e];
         if (ring) ring[((long long)b * a.D + d) * H + write_slot] = x[at + e];
     }
-    store_raw(static_cast<IO *>(a.y) + at, pack<IO>(out));
+    *reinterpret_cast<RawT *>(static_cast<IO *>(a.y) + at) = pack<IO>(h);
     *reinterpret_cast<float4 *>(hstate + at) = make_float4(h[0], h[1], h[2], h[3]);
 }
 
 std::atomic<unsigned> g_epoch{0};
 
+// compute units of the current device (cached per device)
+int compute_units() {
+    static int cached[64] = {0};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+    if (!cached[device]) {
+        int count = 0;
+        if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess
+            || count <= 0)
+            count = 256;
+        cached[device] = count;
+    }
+    return cached[device];
+}
+
 template <typename IO>
 int scan_typed(const DiagArgs &a, void *ws, size_t bytes, hipStream_t stream) {
-    const Layout lay = layout(a.B, a.T, a.D, VEC, sizeof(IO));
+    const Layout lay = layout(a.B, a.T, a.D, sizeof(IO));
     if (bytes < lay.total) return fail(MIRA_ERR_ARG, "diag: workspace too small");
+    if ((unsigned long long)a.T * a.D * sizeof(IO) >= OUT_OF_RANGE)
+        return fail(MIRA_DECLINE, "diag: one sequence must hold under 2 GiB of x");
     unsigned epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
     if (epoch == 0) epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
-    const long long blocks = lay.chains * lay.tiles;
-    hipLaunchKernelGGL((diag_scan_kernel<IO, 4>), dim3(blocks), dim3(64), 0, stream, a,
-                       static_cast<unsigned char *>(ws), epoch);
+    // persistent workgroups: one per CU in all, spread evenly over the chains
+    const long long target = 1LL * compute_units();
+    const int groups_per_chain = (int)std::max<long long>(
+        1, std::min<long long>(lay.tiles, (target + lay.chains - 1) / lay.chains));
+    const long long blocks = lay.chains * groups_per_chain;
+    hipLaunchKernelGGL((diag_scan_kernel<IO, 4>), dim3(blocks), dim3((STREAMS + 1) * 64), 0,
+                       stream, a, static_cast<unsigned char *>(ws), epoch, groups_per_chain);
     return check_launch("diag_scan");
 }
 
@@ -522,12 +565,10 @@ int step_typed(const DiagArgs &a, float *h, hipStream_t stream) {
     return check_launch("diag_step");
 }
 
-int vec_of(int) { return VEC; }
-
 }  // namespace
 
 size_t diag_workspace(int B, int T, int D, int dtype) {
-    return layout(B, T, D, vec_of(dtype), dtype == MIRA_F32 ? 4 : 2).total;
+    return layout(B, T, D, dtype == MIRA_F32 ? 4 : 2).total;
 }
 
 int diag_scan_launch(const DiagArgs &a, void *ws, size_t bytes, hipStream_t stream) {
