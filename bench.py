@@ -34,6 +34,9 @@ def parse():
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--decode-steps", type=int, default=128)
+    parser.add_argument("--calibrate", action="store_true",
+                        help="also run an elementwise kernel of known traffic (reads and writes "
+                             "128 MiB each) five times, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return parser.parse_args()
 
 
@@ -192,12 +195,22 @@ def main():
                                       / decode["elapsed"] / 1e9, 1),
                    "frac_of_hbm": round(decode["per_step_bytes"] * decode["steps"]
                                         / decode["elapsed"] / 1e9 / HBM_PEAK_GBS, 4),
-                   "gla_step_kernel_us": round(decode["gla_kernel_s"] * 1e6, 2),
-                   "gla_step_GBps": round(gla_achieved, 1)},
+                   "roofline": {"bound": "hbm", "kernel": "gla_step_kernel",
+                                "achieved": round(gla_achieved, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(gla_achieved / HBM_PEAK_GBS, 4),
+                                "traffic": traffic_from_profiles("gla_step_kernel"),
+                                "kernel_us": round(decode["gla_kernel_s"] * 1e6, 2),
+                                "algorithmic_bytes": decode["gla_bytes"]}},
         "watchdog": prefill["watchdog"],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_leg()
+    if args.calibrate:
+        source = torch.ones(64 << 20, device="cuda", dtype=torch.bfloat16)
+        target = torch.empty_like(source)
+        for _ in range(5):
+            torch.add(source, 1.0, out=target)
+        torch.cuda.synchronize()
     print(json.dumps(line), flush=True)
 
 

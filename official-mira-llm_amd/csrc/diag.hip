@@ -151,7 +151,8 @@ __device__ __forceinline__ void set_flag(unsigned *flag, unsigned value) {
 }
 
 // Workspace layout (bytes): [0,256) watchdog word | counters[chains] | flags[chains*tiles]
-// | aggregates (A,H)[chains*tiles*TILE_C] | inclusive H[chains*tiles*TILE_C]
+// | aggregates (A,H)[chains*tiles][VEC][64 lanes] | inclusive H[chains*tiles][VEC][64 lanes]
+// (records lane-minor, so a wave's record accesses are contiguous and coalesce)
 struct Layout {
     long long chains, tiles, tile_c;
     size_t counters, flags, agg, inc, total;
@@ -251,7 +252,7 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
                     hin[e] = (dact && a.h0) ? a.h0[(long long)b * a.D + d0 + e] : 0.0f;
             } else {
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) publish_pair(agg + slot * TILE_C + lane * VEC + e, At[e], Ht[e]);
+                for (int e = 0; e < VEC; ++e) publish_pair(agg + (slot * VEC + e) * 64 + lane, At[e], Ht[e]);
                 stores_complete();
                 if (lane == 0) set_flag(flags + slot, tag | 1u);
                 // look back, WINDOW predecessors per round: lane j < WINDOW polls base - j
@@ -286,11 +287,11 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
 #pragma unroll
                     for (int g = 0; g < WINDOW; ++g) {
                         if (g < count) {
-                            const long long record = ((long long)chain * lay.tiles + base - g) * TILE_C + lane * VEC;
+                            const long long record = ((long long)chain * lay.tiles + base - g) * TILE_C + lane;
 #pragma unroll
                             for (int e = 0; e < VEC; ++e)
-                                rec[g][e] = g < first_inclusive ? read_pair(agg + record + e)
-                                                                : make_float2(0.0f, read_value(inc + record + e));
+                                rec[g][e] = g < first_inclusive ? read_pair(agg + record + e * 64)
+                                                                : make_float2(0.0f, read_value(inc + record + e * 64));
                         }
                     }
 #pragma unroll
@@ -313,7 +314,7 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
             }
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                publish_value(inc + slot * TILE_C + lane * VEC + e, fmaf(At[e], hin[e], Ht[e]));
+                publish_value(inc + (slot * VEC + e) * 64 + lane, fmaf(At[e], hin[e], Ht[e]));
                 s_hin[i & 1][e][lane] = hin[e];
             }
             stores_complete();
