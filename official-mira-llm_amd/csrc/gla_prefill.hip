@@ -72,6 +72,7 @@ int prefill_typed(const GlaArgs &a, hipStream_t stream) {
 size_t gla_workspace(int, int, int, int, int) { return 0; }
 
 int gla_chunked_launch(const GlaArgs &a, void *, size_t, hipStream_t stream) {
+    if (gla_chunk_applies(a)) return gla_chunk_launch(a, stream);
     switch (a.dtype) {
         case MIRA_F32: return prefill_typed<float>(a, stream);
         case MIRA_BF16: return prefill_typed<bf16_t>(a, stream);

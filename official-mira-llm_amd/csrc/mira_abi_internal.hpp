@@ -72,5 +72,7 @@ struct GlaArgs {
 int gla_step_launch(const GlaArgs &a, hipStream_t stream);
 size_t gla_workspace(int B, int T, int H, int dk, int dv);
 int gla_chunked_launch(const GlaArgs &a, void *workspace, size_t bytes, hipStream_t stream);
+bool gla_chunk_applies(const GlaArgs &a);
+int gla_chunk_launch(const GlaArgs &a, hipStream_t stream);
 
 }  // namespace mira

@@ -126,3 +126,49 @@ def test_cfg3_full_size_sampled_heads(torch_mod, plugin):
                                           to_numpy(g[b:b + 1, :, h:h + 1]))
         assert scaled(to_numpy(o[b:b + 1, :, h:h + 1]), want_o) <= HALF_SCALED
         assert scaled(to_numpy(ST[b:b + 1, h:h + 1]), want_S) <= 1e-3
+
+
+def test_prefill_bf16_grouped_heads(torch_mod, plugin):
+    """B*H a multiple of 8 places a head's four value blocks on one XCD (the other block order):
+    against the fp64 recurrence, with a ragged last chunk."""
+    torch = torch_mod
+    q, k, v, g, S0 = _inputs(11, 2, 130, 4)
+    td = torch.bfloat16
+    o, ST = plugin.gla_chunked(to_device(q, td), to_device(k, td), to_device(v, td), to_device(g),
+                               state=to_device(S0), return_state=True)
+    want_o, want_S = Bl.gla_recurrent(rounded(q, td), rounded(k, td), rounded(v, td), g, S0)
+    assert scaled(to_numpy(o), want_o) <= HALF_SCALED
+    assert scaled(to_numpy(ST), want_S) <= 1e-3
+
+
+def test_prefill_bf16_unaligned_rows(torch_mod, plugin):
+    """q, k, v that start 2 bytes off a 16-byte boundary take the per-row kernel; same answer."""
+    torch = torch_mod
+    q, k, v, g, S0 = _inputs(12, 1, 70, 2)
+    td = torch.bfloat16
+
+    def shifted(a):
+        flat = torch.empty(a.size + 8, device="cuda", dtype=td)
+        view = flat[1:1 + a.size].view(a.shape)
+        view.copy_(to_device(a, td))
+        assert view.data_ptr() % 16 != 0
+        return view
+
+    o, ST = plugin.gla_chunked(shifted(q), shifted(k), shifted(v), to_device(g),
+                               state=to_device(S0), return_state=True)
+    want_o, want_S = Bl.gla_recurrent(rounded(q, td), rounded(k, td), rounded(v, td), g, S0)
+    assert scaled(to_numpy(o), want_o) <= HALF_SCALED
+    assert scaled(to_numpy(ST), want_S) <= 1e-3
+
+
+def test_decode_equals_prefill_bf16(torch_mod, plugin):
+    """bf16: 70 decode steps against one chunked prefill over the same tokens."""
+    torch = torch_mod
+    td = torch.bfloat16
+    q, k, v, g, S0 = _inputs(13, 1, 70, 2)
+    qd, kd, vd, gd = to_device(q, td), to_device(k, td), to_device(v, td), to_device(g)
+    o, ST = plugin.gla_chunked(qd, kd, vd, gd, state=to_device(S0), return_state=True)
+    S = to_device(S0).clone()
+    outs = [plugin.gla_step(qd[:, t], kd[:, t], vd[:, t], gd[:, t], S) for t in range(70)]
+    assert scaled(to_numpy(torch.stack(outs, 1)), to_numpy(o)) <= HALF_SCALED
+    assert scaled(to_numpy(S), to_numpy(ST)) <= 1e-3
