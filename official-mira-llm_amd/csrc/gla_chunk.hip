@@ -10,7 +10,7 @@
 // One workgroup (8 waves) owns one (b, head, block of 32 value columns) and walks the chunks in
 // order; the 4 blocks of a head sit on one XCD, so their shared q and k reads meet in its L2.
 // Each chunk's q and k (token-major) and V^T (raw, and decayed as a bf16 pair) are staged in LDS
-// by all waves from whole-row HBM loads issued one chunk ahead. Roles per chunk:
+// by all waves from whole-row HBM loads. Roles per chunk:
 //   waves 0-2  one 32x32 tile each of the masked scores P^T (tiles (s,t) = (0,0), (1,1), (0,1);
 //              the (1,0) tile is all masked) on v_mfma_f32_32x32x16_bf16, then V^T P^T for that
 //              tile with the scores still in registers: an accumulator's 4-row groups are exactly
@@ -21,8 +21,8 @@
 // Partial output tiles meet in LDS; waves 0 and 1 add them up and store the chunk's outputs as
 // whole 64-byte row pieces while the next chunk is computed. LDS buffers that cross the one
 // barrier per chunk are double buffered by chunk parity (the decay table G, written two chunks
-// ahead, is triple buffered). Global loads are raw buffer loads whose out-of-range offsets
-// return zeros past the last token; stores past it are dropped the same way.
+// ahead, is triple buffered). Global loads run two chunks ahead as raw buffer loads whose
+// out-of-range offsets return zeros past the last token; stores past it are dropped the same way.
 //
 // Precision: the state recurrence is float32; the decayed values v e^(G_L - G_s) enter the
 // state update as a bf16 high part plus its bf16 rounding remainder (~2^-16 relative), so the
@@ -57,7 +57,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 struct alignas(16) Shared {
     uint16_t q[2][L][QS];          // Q of the chunk, [token][k]
     uint16_t k[2][L][QS];          // K of the chunk, [token][k]
-    uint16_t vt[2][VB][TS];        // V^T of the chunk, [v][token]
+    uint16_t vt[2][VB][TS];        // V^T of the chunk, [vrow(v)][token]
     uint16_t vh[2][VB][TS];        // (V e^(G_L - G_s))^T, bf16 high part
     uint16_t vl[2][VB][TS];        // its bf16 rounding remainder
     uint16_t s[2][VB][QS];         // bf16 copy of the state entering the chunk, [v][k]
@@ -65,6 +65,10 @@ struct alignas(16) Shared {
     uint16_t out[2][32][OS];       // waves 0, 1: a finished output tile, [token][v]
     float G[3][L];                 // in-chunk cumulative log-decay
 };
+
+// LDS row of value column v in the V^T tiles: rows are permuted (v = 8p + e -> 4e + p) so that
+// the staging writes of one wave (16 tokens x 4 pieces of 8 columns) hit distinct banks
+__device__ __forceinline__ int vrow(int v) { return 4 * (v & 7) + (v >> 3); }
 
 // accumulator element i of a 32x32 MFMA tile sits at row drow(lane, i), column lane % 32
 __device__ __forceinline__ int drow(int lane, int i) {
@@ -126,7 +130,8 @@ __device__ __forceinline__ void lds_barrier() {
 
 __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
     __shared__ Shared sh;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index as a scalar: role branches and buffer resources stay uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
 
     int bh, vb;
@@ -154,37 +159,39 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         return t < a.T ? (unsigned)t * row + within : OUT_OF_RANGE;
     };
 
-    // ---- staging: wave w loads tokens [16 (w % 4), +16) of q (w < 4) or k (w >= 4) as 4
-    // row-quads (lane: token 4 r + lane / 16, 16-byte piece lane % 16); waves 4-7 also V tokens
-    // [16 (w - 4), +16) (lane: token lane / 4, piece lane % 4); wave 4 the decays two chunks ahead
+    // ---- staging, two chunks ahead: wave w loads tokens [16 (w % 4), +16) of q (w < 4) or k
+    // (w >= 4) as 4 row-quads (lane: token 4 r + lane / 16, 16-byte piece lane % 16); waves 4-7
+    // also V tokens [16 (w - 4), +16) (lane: token lane / 4, piece lane % 4); wave 4 the decays of
+    // the chunk after. Two register sets alternate by chunk parity.
     const bool loads_q = wave < 4;
     const int kb = wave - 4;                                          // state waves' key block
-    u32x4 pre[4], pv = {0, 0, 0, 0};
-    float pg = 0.0f;
-    auto load_chunk = [&](int chunk) {
-        const int t0 = chunk * L + 16 * (wave & 3);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            pre[r] = __builtin_amdgcn_raw_buffer_load_b128(
-                loads_q ? qr : kr, token_offset(t0 + 4 * r + (lane >> 4), (lane & 15) * 16), 0, 0);
-        if (!loads_q)
-            pv = __builtin_amdgcn_raw_buffer_load_b128(
-                vr, token_offset(t0 + (lane >> 2), (lane & 3) * 16), 0, 0);
-    };
+    struct Staged { u32x4 rows[4], v; float g; };
+    Staged set0, set1;
     auto load_decay = [&](int chunk) {
         const int t = chunk * L + lane;
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              gr, t < a.T ? (unsigned)t * a.H * 4 : OUT_OF_RANGE, 0, 0));
     };
+    auto load_chunk = [&](Staged &in, int chunk) {
+        const int t0 = chunk * L + 16 * (wave & 3);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            in.rows[r] = __builtin_amdgcn_raw_buffer_load_b128(
+                loads_q ? qr : kr, token_offset(t0 + 4 * r + (lane >> 4), (lane & 15) * 16), 0, 0);
+        if (!loads_q)
+            in.v = __builtin_amdgcn_raw_buffer_load_b128(
+                vr, token_offset(t0 + (lane >> 2), (lane & 3) * 16), 0, 0);
+        if (wave == 4) in.g = load_decay(chunk + 1);
+    };
     float gl = 1.0f;                                                  // state waves: e^(G_L)
-    // stage chunk n from the registers; G_s, G_L from the decay table (or `local` in the prologue)
-    auto stage = [&](int n, const float *local) {
+    // stage chunk n from registers; G_s, G_L from the decay table (or `local` in the prologue)
+    auto stage = [&](int n, const Staged &in, const float *local) {
         const int buf = n & 1, row0 = 16 * (wave & 3);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             uint16_t *dst = loads_q ? &sh.q[buf][row0 + 4 * r + (lane >> 4)][(lane & 15) * 8]
                                     : &sh.k[buf][row0 + 4 * r + (lane >> 4)][(lane & 15) * 8];
-            *reinterpret_cast<u32x4 *>(dst) = pre[r];
+            *reinterpret_cast<u32x4 *>(dst) = in.rows[r];
         }
         if (!loads_q) {
             const int s = row0 + (lane >> 2), v0 = 8 * (lane & 3);
@@ -194,20 +201,21 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
             const float scale = __builtin_amdgcn_exp2f((GL - Gs) * LOG2E);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint16_t raw = half_of(pv, e);
+                const uint16_t raw = half_of(in.v, e);
                 const float w = from_bf16(raw) * scale;
                 const uint16_t hi = to_bf16(w);
-                sh.vt[buf][v0 + e][s] = raw;
-                sh.vh[buf][v0 + e][s] = hi;
-                sh.vl[buf][v0 + e][s] = to_bf16(w - from_bf16(hi));
+                sh.vt[buf][vrow(v0 + e)][s] = raw;
+                sh.vh[buf][vrow(v0 + e)][s] = hi;
+                sh.vl[buf][vrow(v0 + e)][s] = to_bf16(w - from_bf16(hi));
             }
         }
     };
 
-    // ---- prologue: chunk 0 staged, decay tables of chunks 0 and 1
+    // ---- prologue: chunk 0 staged, chunk 1 loading, decay tables of chunks 0 and 1
     f32x16 S = {};                                                    // state waves
     const long long srow = ((long long)bh * DV + vb * VB + col) * DK + 32 * kb + 4 * half;
-    load_chunk(0);
+    load_chunk(set0, 0);
+    load_chunk(set1, 1);
     if (!loads_q) {
         if (a.S0) {
 #pragma unroll
@@ -219,18 +227,18 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         const float G0 = wave_prefix_sum(load_decay(0));
         if (kb == 0) {
             sh.G[0][lane] = G0;
-            sh.G[1][lane] = wave_prefix_sum(load_decay(1));
+            sh.G[1][lane] = wave_prefix_sum(set0.g);
         }
         const float local[2] = {__shfl(G0, 16 * kb + (lane >> 2), 64),
                                 __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                               __builtin_bit_cast(int, G0), 63))};
-        stage(0, local);
+        stage(0, set0, local);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<u32x2 *>(&sh.s[0][col][32 * kb + 8 * j + 4 * half]) =
                 u32x2{pack_bf16(S[4 * j], S[4 * j + 1]), pack_bf16(S[4 * j + 2], S[4 * j + 3])};
     } else {
-        stage(0, nullptr);
+        stage(0, set0, nullptr);
     }
     lds_barrier();
 
@@ -240,9 +248,10 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         const int buf = chunk & 1;
         f32x16 total = kept;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            total[i] += sh.part[buf][wave == 0 ? 1 : 2][i][lane];
-            if (wave == 1) total[i] += sh.part[buf][0][i][lane];
+        for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][wave == 0 ? 1 : 2][i][lane];
+        if (wave == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][0][i][lane];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -258,11 +267,11 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         }
     };
 
-    for (int c = 0; c < chunks; ++c) {
+    // iteration c: load chunk c + 2 into `fill`, compute chunk c, stage chunk c + 1 from `use`
+    auto iteration = [&](int c, Staged &fill, const Staged &use) {
         const int buf = c & 1;
         const float *G = sh.G[c % 3];
-        load_chunk(c + 1);
-        if (wave == 4) pg = load_decay(c + 2);
+        load_chunk(fill, c + 2);
         if (wave < 3) {
             if (wave < 2 && c > 0) finish(c - 1);
             const int sb = wave == 1 ? 1 : 0, tb = wave == 0 ? 0 : 1;
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
                 }
                 const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16(p[0], p[1]),
                                                                  pack_bf16(p[2], p[3])});
-                out = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(lds_operand4(&sh.vt[buf][col][s0]),
+                out = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(lds_operand4(&sh.vt[buf][vrow(col)][s0]),
                                                                pb, out, 0, 0, 0);
             }
             if (wave == 2) {
@@ -324,9 +333,9 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     kop[i] = __builtin_bit_cast(__bf16, sh.k[buf][s0 + i][32 * kb + col]);
-                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vh[buf][col][s0]),
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vh[buf][vrow(col)][s0]),
                                                             S, 0, 0, 0);
-                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vl[buf][col][s0]),
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vl[buf][vrow(col)][s0]),
                                                             S, 0, 0, 0);
             }
 #pragma unroll
@@ -335,10 +344,14 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
                     u32x2{pack_bf16(S[4 * j], S[4 * j + 1]), pack_bf16(S[4 * j + 2], S[4 * j + 3])};
         }
         if (c + 1 < chunks) {
-            stage(c + 1, nullptr);
-            if (wave == 4) sh.G[(c + 2) % 3][lane] = wave_prefix_sum(pg);
+            stage(c + 1, use, nullptr);
+            if (wave == 4) sh.G[(c + 2) % 3][lane] = wave_prefix_sum(use.g);
         }
         lds_barrier();
+    };
+    for (int c = 0; c < chunks; c += 2) {
+        iteration(c, set0, set1);
+        if (c + 1 < chunks) iteration(c + 1, set1, set0);
     }
     if (wave < 2) finish(chunks - 1);
     if (!loads_q && a.ST) {
