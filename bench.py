@@ -8,7 +8,9 @@ resident in HBM. A step is one mira_diag_conv_scan launch over the whole batch; 
 tokens/s over exactly K timed steps. Beside it: the decode leg (`configs[3]`, batch 256,
 128 steps of conv+diag and GLA matrix-state updates), the roofline of the dominant kernel from
 HIP events on the launch stream, and the CPU oracle timed on the host's cores on a bounded
-sample of the same workload. Prints one JSON line.
+sample of the same workload. Also reported, not headline: the GLA chunked prefill (`configs[2]`,
+% HBM and % MFMA) and the reference operator matrix_lattice_iir at the cfg5 mixer geometry
+(K=2, M=64). Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -125,6 +127,75 @@ def decode_leg(torch, mira, steps):
             "gla_kernel_s": gla_s, "gla_bytes": gla_bytes}
 
 
+def gla_prefill_leg(torch, mira, steps, warmup):
+    """the matrix-state chunked scan (GLA), bf16 q/k/v, fp32 state, chunk 64,
+    B=4 T=8192 H=16 d=128, carried-in and returned state. One step = one mira_gla_chunked launch."""
+    B, T, H, d = 4, 8192, 16, 128
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, d, device="cuda", generator=g), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, d, device="cuda", generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, T, H, d, device="cuda", generator=g).bfloat16()
+    gd = torch.rand(B, T, H, device="cuda", generator=g) * -0.099 - 0.001
+    S0 = torch.randn(B, H, d, d, device="cuda", generator=g) * 0.1
+    for _ in range(warmup):
+        mira.gla_chunked(q, k, v, gd, state=S0, return_state=True)
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        mira.gla_chunked(q, k, v, gd, state=S0, return_state=True)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_s = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e-3 / steps
+    algorithmic = B * T * H * d * 2 * 4 + B * T * H * 4 + B * H * d * d * 4 * 2
+    flops = B * T * H * 6 * d * d      # per (token, head): 2d^2 state update, 2d^2 readout, 2d^2 intra
+    return {"tokens": B * T, "steps": steps, "elapsed": elapsed, "kernel_s": kernel_s,
+            "algorithmic": algorithmic, "flops": flops}
+
+
+def lattice_leg(torch, mira, steps, warmup):
+    """The reference operator itself, matrix_lattice_iir (model/mira_mixer.py:246-387), at the
+    cfg5 mixer geometry (lattice_d_e 2048, order 2, memory 64; B=4 T=2048), bf16 in/out, fp32
+    state in and out, arch cauchy_x_hyperbolic. Bytes per call (reference-native):
+    B*T*C*2*(3K+4) + B*T*2*M*(K+2) + 2*B*K*C*M*4; fp32 flops B*T*C*M*(9K+4)."""
+    B, T, C, K, M = 4, 2048, 2048, 2, 64
+    g = torch.Generator(device="cuda").manual_seed(3)
+    bf = torch.bfloat16
+    x = (torch.randn(B, T, C, device="cuda", generator=g) * 0.15).to(bf)
+    alpha = (torch.randn(B, T, C, K, device="cuda", generator=g) * 0.12).to(bf)
+    beta = (torch.randn(B, T, C, K, device="cuda", generator=g) * 0.12).to(bf)
+    rho = (torch.randn(B, T, C, K + 1, device="cuda", generator=g) * 0.12).to(bf)
+    gamma = torch.randn(B, T, C, device="cuda", generator=g).to(bf)
+    write = torch.nn.functional.silu(torch.randn(B, T, M, device="cuda", generator=g)).to(bf)
+    read = (torch.randn(B, T, K + 1, M, device="cuda", generator=g) * 0.12).to(bf)
+    state = torch.randn(B, K, C, M, device="cuda", generator=g) * 0.1
+
+    def call():
+        return mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta,
+                                       state=state, return_state=True)
+
+    for _ in range(warmup):
+        call()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        starts[i].record(stream)
+        call()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    call_s = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e-3 / steps
+    nbytes = B * T * C * 2 * (3 * K + 4) + B * T * 2 * M * (K + 2) + 2 * B * K * C * M * 4
+    flops = B * T * C * M * (9 * K + 4)
+    return {"tokens": B * T, "call_s": call_s, "bytes": nbytes, "flops": flops,
+            "shape": f"B={B} T={T} C={C} K={K} M={M}"}
+
+
 def cpu_leg(budget_s=12.0):
     """The oracle's restatement of the reference CPU mixer (the batched per-token formulation of
     model/mira_mixer.py:319-387, numpy float32) on the cfg2 workload realised as the K=1 lattice,
@@ -169,6 +240,9 @@ def main():
         sys.exit(1)
     prefill = prefill_leg(torch, mira, args.steps, args.warmup)
     decode = decode_leg(torch, mira, args.decode_steps)
+    gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3)
+    gla_hbm = gla["algorithmic"] / gla["kernel_s"] / 1e9
+    lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2)
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
     traffic = traffic_from_profiles("diag_scan_kernel")
     gla_achieved = decode["gla_bytes"] / decode["gla_kernel_s"] / 1e9
@@ -201,6 +275,31 @@ def main():
                                 "traffic": traffic_from_profiles("gla_step_kernel"),
                                 "kernel_us": round(decode["gla_kernel_s"] * 1e6, 2),
                                 "algorithmic_bytes": decode["gla_bytes"]}},
+        "matrix_state_prefill": {
+            "metric": "GLA chunked prefill tokens/s (cfg3: B=4 T=8192 H=16 d=128 bf16, chunk 64)",
+            "unit": "tokens/s", "value": gla["tokens"] * gla["steps"] / gla["elapsed"],
+            "roofline": {"bound": "hbm", "kernel": "gla_chunk_kernel",
+                         "achieved": round(gla_hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gla_hbm / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_from_profiles("gla_chunk_kernel"),
+                         "kernel_us": round(gla["kernel_s"] * 1e6, 2),
+                         "algorithmic_bytes": gla["algorithmic"]},
+            "mfma": {"achieved": round(gla["flops"] / gla["kernel_s"] / 1e12, 1),
+                     "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(gla["flops"] / gla["kernel_s"] / 1e12 / 2500.0, 4),
+                     "flops": gla["flops"]}},
+        "lattice_operator": {
+            "metric": "matrix_lattice_iir tokens/s at the cfg5 mixer geometry, bf16",
+            "shape": lat["shape"], "unit": "tokens/s", "value": lat["tokens"] / lat["call_s"],
+            "call_us": round(lat["call_s"] * 1e6, 1),
+            "hbm": {"achieved": round(lat["bytes"] / lat["call_s"] / 1e9, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(lat["bytes"] / lat["call_s"] / 1e9 / HBM_PEAK_GBS, 4),
+                    "algorithmic_bytes": lat["bytes"]},
+            "valu": {"achieved": round(lat["flops"] / lat["call_s"] / 1e12, 1),
+                     "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(lat["flops"] / lat["call_s"] / 1e12 / 157.3, 4),
+                     "flops": lat["flops"]}},
         "watchdog": prefill["watchdog"],
     }
     if not args.no_cpu:

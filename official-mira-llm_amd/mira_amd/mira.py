@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import math
 import os
+import threading
 
 import torch
 
@@ -47,6 +48,7 @@ GLA_DIM = 128
 USED = {"forward": 0, "backward": 0, "step": 0, "diag": 0, "gla": 0}
 REPORTED = set()
 _WORKSPACES = {}
+_WORKSPACE_LOCK = threading.Lock()      # autograd / DataParallel threads may launch
 
 
 def _row_stride(tensor, tokens):
@@ -129,11 +131,12 @@ def workspace(kind, device, nbytes, zero=False):
         return None
     stream = torch.cuda.current_stream(device).cuda_stream
     key = (kind, device.index, stream)
-    buffer = _WORKSPACES.get(key)
-    if buffer is None or buffer.numel() < nbytes:
-        size = max(int(nbytes), 1 << 20)
-        buffer = (torch.zeros if zero else torch.empty)(size, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = buffer
+    with _WORKSPACE_LOCK:
+        buffer = _WORKSPACES.get(key)
+        if buffer is None or buffer.numel() < nbytes:
+            size = max(int(nbytes), 1 << 20)
+            buffer = (torch.zeros if zero else torch.empty)(size, dtype=torch.uint8, device=device)
+            _WORKSPACES[key] = buffer
     return buffer
 
 
