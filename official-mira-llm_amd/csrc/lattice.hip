@@ -17,8 +17,11 @@
 //            the last chunk stores the final state. With one chunk this is the whole scan, and at
 //            T = 1 it is the decode step.
 // A block is 256 threads = G channels x L lanes; lane l of a channel owns M/L memory slots, so a
-// channel's K x M state lives in registers. The write and read vectors s, nu are per (b, t) and
-// shared by every channel, so a block stages a tile of TT tokens of them in LDS.
+// channel's K x M state lives in registers. Per tile of TT tokens the block stages in LDS the
+// write and read vectors s, nu (per (b, t), shared by every channel) and, per (token, channel),
+// the stage coefficients r cos / r sin, x, rho and the gate: the stage maps are evaluated once per
+// channel by one thread instead of by each of the channel's L lanes, and the tile's loads are
+// issued together. Outputs of a tile leave through LDS as whole channel rows.
 #include "mira_device.hpp"
 #include "mira_abi_internal.hpp"
 
@@ -36,10 +39,17 @@ __host__ __device__ constexpr int lanes_for(int K, int M) {
     return L;
 }
 
+// Floats of per-(token, channel) coefficients staged per token: r cos and r sin of the K stages
+// and x (summary), plus rho[K+1] and the SiLU gate (replay).
+__host__ __device__ constexpr int coef_count(int K, bool readout) {
+    return readout ? 3 * K + 3 : 2 * K + 1;
+}
+
 __host__ __device__ constexpr int tile_for(int K, int M) {
-    // tokens of s and nu staged per LDS tile: <= 16 KiB of floats, <= 16 tokens
-    int t = 16;
-    while (t > 1 && t * (K + 2) * M * 4 > 16384) t /= 2;
+    // tokens staged per LDS tile: s and nu <= 16 KiB, the coefficient tile <= 24 KiB, <= 8 tokens
+    int t = 8;
+    const int G = BLOCK / lanes_for(K, M);
+    while (t > 1 && (t * (K + 2) * M * 4 > 16384 || t * coef_count(K, true) * G * 4 > 24576)) t /= 2;
     return t;
 }
 
@@ -52,15 +62,54 @@ __device__ __forceinline__ int slot(int lane, int v) {
     else return v * L + lane;
 }
 
-template <typename IO, int K>
-__device__ __forceinline__ void load_stage(const LatticeArgs &a, long long row, int c,
-                                           int radius_kind, int rotation_kind,
-                                           float (&rc)[K], float (&rs)[K]) {
-    const IO *alpha = static_cast<const IO *>(a.alpha) + row * a.alpha_row + (long long)c * K;
-    const IO *beta = static_cast<const IO *>(a.beta) + row * a.beta_row + (long long)c * K;
+// Sum over the L lanes of a channel group (adjacent lanes): cross-lane DPP within a quad,
+// then butterflies through the LDS crossbar for wider groups.
+template <int L>
+__device__ __forceinline__ float lane_sum(float v) {
+    if constexpr (L >= 2)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                                0xB1, 0xf, 0xf, false));
+    if constexpr (L >= 4)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                                0x4E, 0xf, 0xf, false));
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-        stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc[k], rs[k]);
+    for (int offset = 4; offset < L; offset <<= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+// Stage one token tile of a channel group: per (token, channel) the stage coefficients (once per
+// channel, not once per lane), x, and for the readout rho and the gate; per token the valid flag.
+// Layout coef[token][quantity][channel] so that a wave's reads of one quantity are contiguous.
+template <typename IO, int K, bool READOUT>
+__device__ __forceinline__ void stage_coefficient_tile(const LatticeArgs &a, int b, int tile, int n,
+                                                       int c0, int G, float *coef,
+                                                       unsigned char *valid) {
+    constexpr int NC = coef_count(K, READOUT);
+    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    for (int i = threadIdx.x; i < n * G; i += BLOCK) {
+        const int tt = i / G, cl = i % G, c = c0 + cl;
+        float *dst = coef + tt * NC * G + cl;
+        if (c >= a.C) continue;
+        const long long row = (long long)b * a.T + tile + tt;
+        const IO *alpha = static_cast<const IO *>(a.alpha) + row * a.alpha_row + (long long)c * K;
+        const IO *beta = static_cast<const IO *>(a.beta) + row * a.beta_row + (long long)c * K;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float rc, rs;
+            stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc, rs);
+            dst[k * G] = rc;
+            dst[(K + k) * G] = rs;
+        }
+        dst[2 * K * G] = load(static_cast<const IO *>(a.x) + row * a.x_row + c);
+        if constexpr (READOUT) {
+            const IO *rho = static_cast<const IO *>(a.rho) + row * a.rho_row + (long long)c * (K + 1);
+#pragma unroll
+            for (int k = 0; k <= K; ++k) dst[(2 * K + 1 + k) * G] = load(rho + k);
+            dst[(3 * K + 2) * G] = silu(load(static_cast<const IO *>(a.gamma) + row * a.gamma_row + c));
+        }
+    }
+    for (int tt = threadIdx.x; tt < n; tt += BLOCK)
+        valid[tt] = a.valid ? a.valid[(long long)b * a.T + tile + tt] : 1;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -73,6 +122,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
     constexpr int MV = M / L;
     constexpr int KB = (K + L - 1) / L;          // basis columns of Phi per lane
     constexpr int TT = tile_for(K, M);
+    constexpr int NC = coef_count(K, false);
     const int groups = (a.C + G - 1) / G;
     const int summarised = a.chunks - 1;
     int block = blockIdx.x;
@@ -81,11 +131,13 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
     const int chunk_index = block % summarised;
     const int b = block / summarised;
     const int lane = threadIdx.x % L;
-    const int c = group * G + threadIdx.x / L;
+    const int cl = threadIdx.x / L;
+    const int c = group * G + cl;
     const bool active = c < a.C;
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
 
     __shared__ float s_write[TT * M];
+    __shared__ float s_coef[TT * NC * G];
+    __shared__ unsigned char s_valid[TT];
     float V[K][MV];
     float P[K][KB];
 #pragma unroll
@@ -103,14 +155,16 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
         __syncthreads();
         for (int i = threadIdx.x; i < n * M; i += BLOCK)
             s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
+        stage_coefficient_tile<IO, K, false>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
         if (!active) continue;
         for (int tt = 0; tt < n; ++tt) {
-            const long long row = (long long)b * a.T + tile + tt;
-            if (a.valid && !a.valid[row]) continue;
+            if (!s_valid[tt]) continue;
+            const float *cf = s_coef + tt * NC * G + cl;
             float rc[K], rs[K];
-            load_stage<IO, K>(a, row, c, radius_kind, rotation_kind, rc, rs);
-            const float xv = load(static_cast<const IO *>(a.x) + row * a.x_row + c);
+#pragma unroll
+            for (int k = 0; k < K; ++k) { rc[k] = cf[k * G]; rs[k] = cf[(K + k) * G]; }
+            const float xv = cf[2 * K * G];
 #pragma unroll
             for (int v = 0; v < MV; ++v) {
                 float U = xv * s_write[tt * M + slot<M, L>(lane, v)];
@@ -199,6 +253,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     constexpr int G = BLOCK / L;
     constexpr int MV = M / L;
     constexpr int TT = tile_for(K, M);
+    constexpr int NC = coef_count(K, true);
     const int groups = (a.C + G - 1) / G;
     int block = blockIdx.x;
     const int group = block % groups;
@@ -206,12 +261,15 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     const int chunk_index = block % a.chunks;
     const int b = block / a.chunks;
     const int lane = threadIdx.x % L;
-    const int c = group * G + threadIdx.x / L;
+    const int cl = threadIdx.x / L;
+    const int c = group * G + cl;
     const bool active = c < a.C;
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
 
     __shared__ float s_write[TT * M];
     __shared__ float s_read[TT * (K + 1) * M];
+    __shared__ float s_coef[TT * NC * G];
+    __shared__ float s_out[TT * G];
+    __shared__ unsigned char s_valid[TT];
     float V[K][MV];
 #pragma unroll
     for (int k = 0; k < K; ++k)
@@ -234,52 +292,57 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     IO *out = static_cast<IO *>(a.out);
     for (int tile = first; tile < last; tile += TT) {
         const int n = min(TT, last - tile);
-        __syncthreads();
+        __syncthreads();                                       // previous tile's outputs stored
         for (int i = threadIdx.x; i < n * M; i += BLOCK)
             s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
         for (int i = threadIdx.x; i < n * (K + 1) * M; i += BLOCK) {
             const int tt = i / ((K + 1) * M), rest = i % ((K + 1) * M);
             s_read[i] = load(read + ((long long)b * a.T + tile + tt) * a.read_row + rest);
         }
+        stage_coefficient_tile<IO, K, true>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
-        if (!active) continue;
-        for (int tt = 0; tt < n; ++tt) {
-            const long long row = (long long)b * a.T + tile + tt;
-            if (a.valid && !a.valid[row]) {
-                if (lane == 0) out[row * a.C + c] = from_float<IO>(0.0f);
-                continue;
-            }
-            float rc[K], rs[K], rho[K + 1];
-            load_stage<IO, K>(a, row, c, radius_kind, rotation_kind, rc, rs);
-            const IO *rho_row = static_cast<const IO *>(a.rho) + row * a.rho_row + (long long)c * (K + 1);
+        if (active) {
+            for (int tt = 0; tt < n; ++tt) {
+                float y = 0.0f;
+                if (s_valid[tt]) {
+                    const float *cf = s_coef + tt * NC * G + cl;
+                    float rc[K], rs[K], rho[K + 1];
 #pragma unroll
-            for (int k = 0; k <= K; ++k) rho[k] = load(rho_row + k);
-            const float xv = load(static_cast<const IO *>(a.x) + row * a.x_row + c);
-            const float gate = silu(load(static_cast<const IO *>(a.gamma) + row * a.gamma_row + c));
-            const float *nu = s_read + tt * (K + 1) * M;
-            float acc[K + 1];
+                    for (int k = 0; k < K; ++k) { rc[k] = cf[k * G]; rs[k] = cf[(K + k) * G]; }
+                    const float xv = cf[2 * K * G];
 #pragma unroll
-            for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
+                    for (int k = 0; k <= K; ++k) rho[k] = cf[(2 * K + 1 + k) * G];
+                    const float gate = cf[(3 * K + 2) * G];
+                    const float *nu = s_read + tt * (K + 1) * M;
+                    float acc[K + 1];
 #pragma unroll
-            for (int v = 0; v < MV; ++v) {
-                const int m = slot<M, L>(lane, v);
-                float U = xv * s_write[tt * M + m];
+                    for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
 #pragma unroll
-                for (int k = K; k >= 1; --k) {
-                    const float delayed = V[k - 1][v];
-                    const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
-                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
-                    acc[k] = fmaf(level, nu[k * M + m], acc[k]);
-                    if (k < K) V[k][v] = level;
+                    for (int v = 0; v < MV; ++v) {
+                        const int m = slot<M, L>(lane, v);
+                        float U = xv * s_write[tt * M + m];
+#pragma unroll
+                        for (int k = K; k >= 1; --k) {
+                            const float delayed = V[k - 1][v];
+                            const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                            U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                            acc[k] = fmaf(level, nu[k * M + m], acc[k]);
+                            if (k < K) V[k][v] = level;
+                        }
+                        V[0][v] = U;
+                        acc[0] = fmaf(U, nu[m], acc[0]);
+                    }
+#pragma unroll
+                    for (int k = 0; k <= K; ++k) y = fmaf(rho[k], acc[k], y);
+                    y = gate * lane_sum<L>(y);
                 }
-                V[0][v] = U;
-                acc[0] = fmaf(U, nu[m], acc[0]);
+                if (lane == 0) s_out[tt * G + cl] = y;
             }
-            float y = 0.0f;
-#pragma unroll
-            for (int k = 0; k <= K; ++k) y = fmaf(rho[k], acc[k], y);
-            y = group_sum<L>(y);
-            if (lane == 0) out[row * a.C + c] = from_float<IO>(gate * y);
+        }
+        __syncthreads();                                       // the tile's outputs
+        for (int i = threadIdx.x; i < n * G; i += BLOCK) {
+            const int tt = i / G, cc = group * G + i % G;
+            if (cc < a.C) out[((long long)b * a.T + tile + tt) * a.C + cc] = from_float<IO>(s_out[i]);
         }
     }
     if (active && a.state_out && chunk_index == a.chunks - 1) {
