@@ -121,10 +121,10 @@ __device__ __forceinline__ typename Raw<IO>::type pack(const float (&f)[VEC]) {
 }
 
 // PUBLICATION WITHOUT AN L2 WRITE-BACK. A release fence at agent scope writes back the whole L2
-// of the issuing XCD, and a tile publishes twice, so the published records are instead written
-// and read with agent-scope relaxed atomics, which go to the device coherence point instead of
-// the XCD's non-coherent L2; the writer waits for its record stores to complete (vmcnt(0))
-// before it stores the flag, and a reader loads a record only after it has seen the flag.
+// of the issuing XCD, so the published records are instead written and read with agent-scope
+// relaxed atomics, which go to the device coherence point instead of the XCD's non-coherent L2;
+// the writer waits for its record stores to complete (vmcnt(0)) before it stores the flag, and a
+// reader loads a record only after it has seen the flag.
 __device__ __forceinline__ void publish_value(float *p, float v) {
     __hip_atomic_store(reinterpret_cast<unsigned *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
@@ -196,11 +196,12 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
     float *inc = reinterpret_cast<float *>(ws + lay.inc);
 
     __shared__ int s_ticket[4];                      // tickets t_i, ring of four
-    __shared__ float2 s_map[3][STREAMS][VEC][64];    // streaming waves' maps, by i mod 3
-    __shared__ float s_hin[2][VEC][64];              // resolved entering state, by tile parity
-    __shared__ float4 s_b[2][STREAMS][TPW][64];      // b_t = (1 - a_t) u_t of a wave's tokens
+    // the streaming waves' maps of tile i, by i mod 3; once the look-back wave has folded them,
+    // the same slot carries each wave's resolved entering state (.x)
+    __shared__ float2 s_map[3][STREAMS][VEC][64];
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index as a scalar, so the role branch and per-wave loops are uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int chain = blockIdx.x % lay.chains;
     const int cblocks = (a.D + TILE_C - 1) / TILE_C;
     const int b = chain / cblocks;
@@ -208,6 +209,7 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
     const bool dact = d0 < a.D;
     const long long row0 = (long long)b * a.T;
     const unsigned tag = (epoch & 0x3fffffffu) << 2;
+    const unsigned tag_agg = tag | 1u, tag_inc = tag | 2u;           // flag values
     const unsigned last_draw = (unsigned)lay.tiles + 3u * (unsigned)groups_per_chain - 1u;
 
     if (wave == 0) {
@@ -228,99 +230,179 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
         const int t0 = draw(), t1 = draw(), t2 = draw();
         if (lane == 0) { s_ticket[0] = t0; s_ticket[1] = t1; s_ticket[2] = t2; }
         lds_barrier();                                               // P
-        for (int i = 0;; ++i) {
-            const int tile = s_ticket[i & 3];
-            lds_barrier();                                           // X_i: maps of tile i
-            if (tile >= lay.tiles) break;
-            // the tile's map: the streaming waves' maps in token order
-            float At[VEC], Ht[VEC];
+        // the inclusive state of this workgroup's last resolved tile, which its look-backs use
+        // without waiting for its flag
+        long long own_tile = -1;
+        float own_inc[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // the look-back of one tile, WINDOW predecessors per round (lane j < WINDOW polls
+        // base - j): folds published aggregates back to the nearest inclusive state
+        // `first` is the caller's read of the first round's flags (lane j: tile - 1 - j)
+        auto resolve = [&](int tile, float (&hin)[VEC], unsigned first) {
+            float cA[VEC], cH[VEC];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) { At[e] = 1.0f; Ht[e] = 0.0f; }
-            for (int g = 0; g < STREAMS; ++g) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float2 m = s_map[i % 3][g][e][lane];
-                    Ht[e] = fmaf(m.x, Ht[e], m.y);
-                    At[e] *= m.x;
+            for (int e = 0; e < VEC; ++e) { cA[e] = 1.0f; cH[e] = 0.0f; hin[e] = 0.0f; }
+            long long base = tile - 1;
+            unsigned spins = 0;
+            bool fresh = true;
+            while (true) {
+                unsigned status = 2;                                 // before the first tile
+                if (lane < WINDOW && base - lane >= 0) {
+                    const unsigned f = fresh ? first
+                                             : __hip_atomic_load(flags + (long long)chain * lay.tiles + base - lane,
+                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    status = (f & ~3u) == tag ? (f & 3u) : 0u;
+                    if (base - lane == own_tile) status = 2;         // known here, flag or not
                 }
-            }
-            const long long slot = (long long)chain * lay.tiles + tile;
-            float hin[VEC];
-            if (tile == 0) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e)
-                    hin[e] = (dact && a.h0) ? a.h0[(long long)b * a.D + d0 + e] : 0.0f;
-            } else {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) publish_pair(agg + (slot * VEC + e) * 64 + lane, At[e], Ht[e]);
-                stores_complete();
-                if (lane == 0) set_flag(flags + slot, tag | 1u);
-                // look back, WINDOW predecessors per round: lane j < WINDOW polls base - j
-                float cA[VEC], cH[VEC];
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) { cA[e] = 1.0f; cH[e] = 0.0f; hin[e] = 0.0f; }
-                long long base = tile - 1;
-                unsigned spins = 0;
-                while (true) {
-                    unsigned status = 2;                             // before the first tile
-                    if (lane < WINDOW && base - lane >= 0) {
-                        const unsigned f = __hip_atomic_load(flags + (long long)chain * lay.tiles + base - lane,
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        status = (f & ~3u) == tag ? (f & 3u) : 0u;
+                fresh = false;
+                const unsigned long long ready = __ballot(lane < WINDOW && status >= 1);
+                const unsigned long long inclusive = __ballot(lane < WINDOW && status == 2);
+                const int first_inclusive = inclusive ? __builtin_ctzll(inclusive) : WINDOW;
+                const unsigned long long need = (1ull << first_inclusive) - 1ull;
+                if ((ready & need) != need) {
+                    if (++spins > SPIN_LIMIT) {
+                        if (lane == 0)
+                            __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
                     }
-                    const unsigned long long ready = __ballot(lane < WINDOW && status >= 1);
-                    const unsigned long long inclusive = __ballot(lane < WINDOW && status == 2);
-                    const int first_inclusive = inclusive ? __builtin_ctzll(inclusive) : WINDOW;
-                    const unsigned long long need = (1ull << first_inclusive) - 1ull;
-                    if ((ready & need) != need) {
-                        if (++spins > SPIN_LIMIT) {
-                            if (lane == 0)
-                                __hip_atomic_store(watchdog, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(2);
-                        continue;
+                    __builtin_amdgcn_s_sleep(2);
+                    continue;
+                }
+                // the records, nearest first: aggregates, then the inclusive state
+                const int count = first_inclusive < WINDOW ? first_inclusive + 1 : WINDOW;
+                float2 rec[WINDOW][VEC];
+#pragma unroll
+                for (int g = 0; g < WINDOW; ++g) {
+                    if (g < count) {
+                        const long long record = ((long long)chain * lay.tiles + base - g) * TILE_C + lane;
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e)
+                            rec[g][e] = g < first_inclusive ? read_pair(agg + record + e * 64)
+                                      : base - g == own_tile ? make_float2(0.0f, own_inc[e])
+                                                             : make_float2(0.0f, read_value(inc + record + e * 64));
                     }
-                    // the records, nearest first: aggregates, then the inclusive state
-                    const int count = first_inclusive < WINDOW ? first_inclusive + 1 : WINDOW;
-                    float2 rec[WINDOW][VEC];
+                }
 #pragma unroll
-                    for (int g = 0; g < WINDOW; ++g) {
-                        if (g < count) {
-                            const long long record = ((long long)chain * lay.tiles + base - g) * TILE_C + lane;
+                for (int g = 0; g < WINDOW; ++g) {
+                    if (g < count) {
 #pragma unroll
-                            for (int e = 0; e < VEC; ++e)
-                                rec[g][e] = g < first_inclusive ? read_pair(agg + record + e * 64)
-                                                                : make_float2(0.0f, read_value(inc + record + e * 64));
-                        }
-                    }
-#pragma unroll
-                    for (int g = 0; g < WINDOW; ++g) {
-                        if (g < count) {
-#pragma unroll
-                            for (int e = 0; e < VEC; ++e) {
-                                if (g < first_inclusive) {           // fold one more aggregate
-                                    cH[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
-                                    cA[e] *= rec[g][e].x;
-                                } else {                             // the inclusive state
-                                    hin[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
-                                }
+                        for (int e = 0; e < VEC; ++e) {
+                            if (g < first_inclusive) {               // fold one more aggregate
+                                cH[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
+                                cA[e] *= rec[g][e].x;
+                            } else {                                 // the inclusive state
+                                hin[e] = fmaf(cA[e], rec[g][e].y, cH[e]);
                             }
                         }
                     }
-                    if (first_inclusive < WINDOW) break;
-                    base -= WINDOW;
                 }
+                if (first_inclusive < WINDOW) break;
+                base -= WINDOW;
             }
+        };
+        // the inclusive state of `tile` (map At, Ht; entering state hin) to its record, and each
+        // streaming wave's entering state, carried through the maps of the waves before it, to
+        // the .x of the tile's map slot `ring` (read after a later barrier)
+        auto finish_tile = [&](int tile, int ring, const float (&At)[VEC], const float (&Ht)[VEC],
+                               float (&hin)[VEC]) {
+            const long long slot = (long long)chain * lay.tiles + tile;
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                publish_value(inc + (slot * VEC + e) * 64 + lane, fmaf(At[e], hin[e], Ht[e]));
-                s_hin[i & 1][e][lane] = hin[e];
+                own_inc[e] = fmaf(At[e], hin[e], Ht[e]);
+                publish_value(inc + (slot * VEC + e) * 64 + lane, own_inc[e]);
             }
+            own_tile = tile;
+#pragma unroll
+            for (int g = 0; g < STREAMS; ++g) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const float2 m = s_map[ring][g][e][lane];
+                    s_map[ring][g][e][lane].x = hin[e];
+                    hin[e] = fmaf(m.x, hin[e], m.y);
+                }
+            }
+        };
+        // Tile i's aggregate is published after barrier X_i; the tile is resolved one iteration
+        // later, after X_(i+1), when the aggregates of the tiles the other workgroups of the chain
+        // drew meanwhile are out too, so a look-back rarely waits. Tile 0 needs no look-back and
+        // is resolved at once. The streaming waves replay tile i after X_(i+2).
+        // The ticket draw is issued first, so its round trip overlaps the others.
+        // Iteration i takes barrier X_i while tile i, i - 1 or i - 2 is one of this workgroup's
+        // tiles -- the streaming waves run the same count.
+        int tile_prev = lay.tiles, tile_prev2 = lay.tiles;           // tiles i - 1, i - 2
+        int announce = lay.tiles;                                    // inclusive written, flag pending
+        float Ap[VEC], Hp[VEC];                                      // tile i - 1's map
+        for (int i = 0;; ++i) {
+            // tickets rise, so once a drawn tile is past the end every later one is too
+            const int tile = (i == 0 || tile_prev < lay.tiles) ? s_ticket[i & 3] : lay.tiles;
+            if (tile >= lay.tiles && tile_prev >= lay.tiles && tile_prev2 >= lay.tiles) break;
+            lds_barrier();                                           // X_i: maps of tile i
+            const bool live = tile < lay.tiles;
+            unsigned drawn = 0;
+            if (live && lane == 0) drawn = atomicAdd(counters + chain, 1u);
+            float At[VEC], Ht[VEC];
+            if (live) {
+                // the tile's map: the streaming waves' maps in token order
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) { At[e] = 1.0f; Ht[e] = 0.0f; }
+#pragma unroll
+                for (int g = 0; g < STREAMS; ++g) {
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) {
+                        const float2 m = s_map[i % 3][g][e][lane];
+                        Ht[e] = fmaf(m.x, Ht[e], m.y);
+                        At[e] *= m.x;
+                    }
+                }
+            }
+            // this tile's records go out first; the first look-back poll is issued behind them, so
+            // one wait covers both round trips (and the inclusive records of the tile resolved in
+            // the previous iteration, whose flag is set now)
+            if (live) {
+                if (tile == 0) {
+                    float hin[VEC];
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e)
+                        hin[e] = (dact && a.h0) ? a.h0[(long long)b * a.D + d0 + e] : 0.0f;
+                    finish_tile(0, i % 3, At, Ht, hin);
+                } else {
+                    const long long slot = (long long)chain * lay.tiles + tile;
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e)
+                        publish_pair(agg + (slot * VEC + e) * 64 + lane, At[e], Ht[e]);
+                }
+            }
+            const bool resolving = tile_prev < lay.tiles && tile_prev != 0;
+            unsigned first = 0;
+            if (resolving && lane < WINDOW && tile_prev - 1 - lane >= 0)
+                first = __hip_atomic_load(flags + (long long)chain * lay.tiles + tile_prev - 1 - lane,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             stores_complete();
-            if (lane == 0) set_flag(flags + slot, tag | 2u);
-            const int t3 = draw();
-            if (lane == 0) s_ticket[(i + 3) & 3] = t3;
+            if (lane == 0) {
+                if (announce < lay.tiles) set_flag(flags + (long long)chain * lay.tiles + announce, tag_inc);
+                if (live) {
+                    set_flag(flags + (long long)chain * lay.tiles + tile, tile == 0 ? tag_inc : tag_agg);
+                    if (drawn == last_draw)
+                        __hip_atomic_store(counters + chain, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    s_ticket[(i + 3) & 3] = (int)drawn;
+                }
+            }
+            announce = lay.tiles;
+            if (resolving) {
+                float hin[VEC];
+                resolve(tile_prev, hin, first);
+                finish_tile(tile_prev, (i + 2) % 3, Ap, Hp, hin);
+                announce = tile_prev;                                // flag set after the next wait
+            }
+            if (live) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) { Ap[e] = At[e]; Hp[e] = Ht[e]; }
+            }
+            tile_prev2 = tile_prev;
+            tile_prev = tile;
+        }
+        if (announce < lay.tiles) {
+            stores_complete();
+            if (lane == 0) set_flag(flags + (long long)chain * lay.tiles + announce, tag_inc);
         }
         return;
     }
@@ -376,10 +458,25 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
             ap[k] = load_pack<IO, NT>(ar, off);
         }
     };
+    // the conv and the decay input of one token: u = w . (x_(t-3), .., x_t) + bias,
+    // b = (1 - a) u; `win` holds the H previous x and is shifted
+    auto token_input = [&](const float (&xf)[VEC], const float (&af)[VEC], float (&win)[H][VEC],
+                           float (&bv)[VEC]) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            float u = bias[e];
+#pragma unroll
+            for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], win[j][e], u);
+            u = fmaf(wv[e][H], xf[e], u);
+            bv[e] = fmaf(-af[e], u, u);
+#pragma unroll
+            for (int j = 0; j + 1 < H; ++j) win[j][e] = win[j + 1][e];
+            win[H - 1][e] = xf[e];
+        }
+    };
     // first pass: conv and decay over the wave's tokens from zero, giving the wave's map (A, H)
-    // and b_t = (1 - a_t) u_t, which goes to LDS for the replay
     auto summarise = [&](const RawT (&xp)[TPW], const RawT (&ap)[TPW], const RawT (&hist)[H],
-                         float4 (&bout)[TPW][64], float (&A)[VEC], float (&h)[VEC]) {
+                         float (&A)[VEC], float (&h)[VEC]) {
         float win[H][VEC];
 #pragma unroll
         for (int j = 0; j < H; ++j) unpack<IO>(hist[j], win[j]);
@@ -388,33 +485,29 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
             float xf[VEC], af[VEC], bv[VEC];
             unpack<IO>(xp[k], xf);
             unpack<IO>(ap[k], af);
+            token_input(xf, af, win, bv);
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                float u = bias[e];
-#pragma unroll
-                for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], win[j][e], u);
-                u = fmaf(wv[e][H], xf[e], u);
-                bv[e] = fmaf(-af[e], u, u);
                 h[e] = fmaf(af[e], h[e], bv[e]);
                 A[e] *= af[e];
-#pragma unroll
-                for (int j = 0; j + 1 < H; ++j) win[j][e] = win[j + 1][e];
-                win[H - 1][e] = xf[e];
             }
-            bout[k][lane] = make_float4(bv[0], bv[1], bv[2], bv[3]);
         }
     };
-    // replay: h = a h + b from the wave's entering state, storing y
-    auto replay = [&](int t0, const RawT (&ap)[TPW], const float4 (&bin)[TPW][64], float (&h)[VEC]) {
+    // second pass: the same tokens from the wave's entering state, recomputing b (bitwise as in
+    // the first pass), storing y
+    auto replay = [&](int t0, const RawT (&xp)[TPW], const RawT (&ap)[TPW], const RawT (&hist)[H],
+                      float (&h)[VEC]) {
+        float win[H][VEC];
+#pragma unroll
+        for (int j = 0; j < H; ++j) unpack<IO>(hist[j], win[j]);
 #pragma unroll
         for (int k = 0; k < TPW; ++k) {
-            float af[VEC];
+            float xf[VEC], af[VEC], bv[VEC];
+            unpack<IO>(xp[k], xf);
             unpack<IO>(ap[k], af);
-            const float4 bq = bin[k][lane];
-            h[0] = fmaf(af[0], h[0], bq.x);
-            h[1] = fmaf(af[1], h[1], bq.y);
-            h[2] = fmaf(af[2], h[2], bq.z);
-            h[3] = fmaf(af[3], h[3], bq.w);
+            token_input(xf, af, win, bv);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) h[e] = fmaf(af[e], h[e], bv[e]);
             store_pack<IO, NT>(yr, offset(t0 + k), pack<IO>(h));
             if (dact && t0 + k == a.T - 1 && a.hT) {
 #pragma unroll
@@ -424,37 +517,33 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
     };
 
     lds_barrier();                                                   // P
-    int tile_prev = lay.tiles, tile_cur = s_ticket[0];
-    RawT xc[TPW], ac[TPW], hc[H];                                    // tile i (map pending)
-    RawT aq[TPW];                                                    // tile i - 1 (replay pending)
-    fetch(tile_cur, xc, ac, hc);
-    for (int i = 0;; ++i) {
-        const int tile_next = s_ticket[(i + 1) & 3];
-        RawT xn[TPW], an[TPW], hn[H];                                // tile i + 1 (loads in flight)
-        fetch(tile_next, xn, an, hn);
+    // Step i: issue tile i+1's loads, summarise tile i, barrier X_i, replay tile i-2 (resolved by
+    // the look-back wave after X_(i-1)). Four register sets rotate, so loads land directly in the
+    // registers they are used from and a tile's packs stay until its replay (no b buffer in LDS).
+    struct Packs { RawT x[TPW], a[TPW], h[H]; };
+    Packs set0, set1, set2, set3;
+    int tile_cur = s_ticket[0], tile_prev = lay.tiles, tile_prev2 = lay.tiles;
+    fetch(tile_cur, set0.x, set0.a, set0.h);
+    auto step = [&](int i, Packs &cur, Packs &next, Packs &old) -> bool {
+        // the look-back wave runs the same rule, so both take the same barriers
+        if (tile_cur >= lay.tiles && tile_prev >= lay.tiles && tile_prev2 >= lay.tiles) return false;
+        const int tile_next = tile_cur < lay.tiles ? s_ticket[(i + 1) & 3] : lay.tiles;
+        fetch(tile_next, next.x, next.a, next.h);
         if (tile_cur < lay.tiles) {
             float A[VEC] = {1.0f, 1.0f, 1.0f, 1.0f}, Hs[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
-            summarise(xc, ac, hc, s_b[i & 1][sw], A, Hs);
+            summarise(cur.x, cur.a, cur.h, A, Hs);
 #pragma unroll
             for (int e = 0; e < VEC; ++e) s_map[i % 3][sw][e][lane] = make_float2(A[e], Hs[e]);
         }
         lds_barrier();                                               // X_i
-        if (tile_prev < lay.tiles) {
-            // entering state of this wave in tile i - 1: the tile's resolved state carried
-            // through the maps of the streaming waves before this one
+        if (tile_prev2 < lay.tiles) {
+            // this wave's entering state in tile i - 2, resolved by the look-back wave
             float h[VEC];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) h[e] = s_hin[(i - 1) & 1][e][lane];
-            for (int g = 0; g < sw; ++g) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float2 m = s_map[(i + 2) % 3][g][e][lane];       // tile i - 1
-                    h[e] = fmaf(m.x, h[e], m.y);
-                }
-            }
-            replay(tile_prev * TILE_T + sw * TPW, aq, s_b[(i - 1) & 1][sw], h);
+            for (int e = 0; e < VEC; ++e) h[e] = s_map[(i + 1) % 3][sw][e][lane].x;
+            replay(tile_prev2 * TILE_T + sw * TPW, old.x, old.a, old.h, h);
             // the ring after this call: the last H stream tokens, each in slot (stream mod H)
-            if (a.ring_out && tile_prev == lay.tiles - 1 && sw == 0 && dact) {
+            if (a.ring_out && tile_prev2 == lay.tiles - 1 && sw == 0 && dact) {
                 const IO *ring_in = static_cast<const IO *>(a.ring_in);
                 IO *ring_out = static_cast<IO *>(a.ring_out);
 #pragma unroll
@@ -473,13 +562,16 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
                 }
             }
         }
-        if (tile_cur >= lay.tiles) break;
+        tile_prev2 = tile_prev;
         tile_prev = tile_cur;
         tile_cur = tile_next;
-#pragma unroll
-        for (int k = 0; k < TPW; ++k) { aq[k] = ac[k]; xc[k] = xn[k]; ac[k] = an[k]; }
-#pragma unroll
-        for (int j = 0; j < H; ++j) hc[j] = hn[j];
+        return true;
+    };
+    for (int i = 0;; i += 4) {
+        if (!step(i, set0, set1, set2)) break;
+        if (!step(i + 1, set1, set2, set3)) break;
+        if (!step(i + 2, set2, set3, set0)) break;
+        if (!step(i + 3, set3, set0, set1)) break;
     }
 }
 
