@@ -26,6 +26,7 @@
 #include "mira_abi_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mira {
 namespace {
@@ -206,6 +207,194 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// summary on the matrix cores (bf16 inputs): per channel the stage maps are affine in the state,
+// V_t = A_t V_(t-1) + b_t U_t with U_t = x_t s_t[m], and A_t, b_t (K x K, K) do not depend on m.
+// So the chunk's carry from a zero state is carry[k][m] = sum_s g_s[k] x_s s_s[m] with
+// g_s = A_L .. A_(s+1) b_s: a backward scan per channel gives g_s and Phi = A_L .. A_1 with
+// O(K^2) work per token instead of O(K M), and the sum over s is a GEMM,
+//     carry[(c, k)][m] = sum_s (g_s[c][k] x_s[c]) . s_s[m],
+// run on v_mfma_f32_32x32x16_bf16 with the left operand split into a bf16 high part and its
+// rounding remainder (float32-level accuracy; s is bf16 already).
+// A block owns 64 rows (c, k) -- 64 / K channels -- and walks the chunk backwards in tiles of 16
+// tokens: stage the tile's stage maps and s^T, scan it backwards, multiply-accumulate.
+// ---------------------------------------------------------------------------------------------
+namespace summary_mfma {
+constexpr int ROWS = 64, TT = 16, TP = TT + 8;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int drow(int lane, int i) { return 8 * (i >> 2) + ((lane >> 5) << 2) + (i & 3); }
+__device__ __forceinline__ bf16x8 operand(const uint16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ uint16_t to_bf16(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+__device__ __forceinline__ float from_bf16(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+}  // namespace summary_mfma
+
+template <int K, int M>
+__global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
+    using namespace summary_mfma;
+    constexpr int G = ROWS / K;                  // channels per block
+    constexpr int CT = M / 32;                   // output column tiles
+    constexpr int TILES = 2 * CT;                // 32 x 32 output tiles (2 row tiles)
+    constexpr int PER_WAVE = (TILES + 3) / 4;
+    const int groups = (a.C + G - 1) / G;
+    const int summarised = a.chunks - 1;
+    int block = blockIdx.x;
+    const int group = block % groups;
+    block /= groups;
+    const int chunk_index = block % summarised;
+    const int b = block / summarised;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int c0 = group * G;
+    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+
+    __shared__ float s_A[TT][G][K * K];          // per (token, channel): A_t, row-major [k][j]
+    __shared__ float s_b[TT][G][K];              // b_t scaled by x_t (the injection of U = s)
+    __shared__ alignas(16) uint16_t s_wT[M][TP]; // s^T of the tile, [m][token]
+    __shared__ alignas(16) uint16_t s_hi[ROWS][TP], s_lo[ROWS][TP];   // g x, [(c, k)][token]
+
+    f32x16 acc[PER_WAVE];
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) acc[q] = f32x16{};
+    // the backward product P = A_L .. A_(s+1), one thread per channel
+    float P[K][K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int j = 0; j < K; ++j) P[k][j] = k == j ? 1.0f : 0.0f;
+
+    const int first = chunk_index * a.chunk;
+    const uint16_t *write = static_cast<const uint16_t *>(a.write);
+    for (int tile = first + a.chunk - TT; tile >= first; tile -= TT) {
+        __syncthreads();                                       // previous tile's operands used
+        // stage maps of the tile as an affine map of (V, U): push the K basis states and U = 1
+        for (int i = tid; i < TT * G; i += BLOCK) {
+            const int tt = i / G, cl = i % G, c = c0 + cl;
+            const long long row = (long long)b * a.T + tile + tt;
+            float Acol[K][K], bv[K];
+            const bool on = c < a.C && (!a.valid || a.valid[row]);
+            if (on) {
+                float rc[K], rs[K];
+                const bf16_t *alpha = static_cast<const bf16_t *>(a.alpha) + row * a.alpha_row + (long long)c * K;
+                const bf16_t *beta = static_cast<const bf16_t *>(a.beta) + row * a.beta_row + (long long)c * K;
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+                    stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc[k], rs[k]);
+                const float xv = load(static_cast<const bf16_t *>(a.x) + row * a.x_row + c);
+#pragma unroll
+                for (int col = 0; col <= K; ++col) {           // col < K: basis state e_col; K: U = 1
+                    float V[K];
+#pragma unroll
+                    for (int k = 0; k < K; ++k) V[k] = (k == col) ? 1.0f : 0.0f;
+                    float U = col == K ? 1.0f : 0.0f;
+#pragma unroll
+                    for (int k = K; k >= 1; --k) {
+                        const float delayed = V[k - 1];
+                        const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                        U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                        if (k < K) V[k] = level;
+                    }
+                    V[0] = U;
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        if (col < K) Acol[k][col] = V[k];
+                        else bv[k] = V[k] * xv;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+#pragma unroll
+                    for (int j = 0; j < K; ++j) Acol[k][j] = k == j ? 1.0f : 0.0f;
+                    bv[k] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+#pragma unroll
+                for (int j = 0; j < K; ++j) s_A[tt][cl][k * K + j] = Acol[k][j];
+                s_b[tt][cl][k] = bv[k];
+            }
+        }
+        // s of the tile, transposed: [m][token]
+        for (int i = tid; i < TT * M; i += BLOCK) {
+            const int tt = i / M, m = i % M;
+            s_wT[m][tt] = write[((long long)b * a.T + tile + tt) * M + m];
+        }
+        __syncthreads();
+        // backward scan: g_s = P b_s x_s, then P = P A_s
+        if (tid < G) {
+#pragma unroll 4
+            for (int tt = TT - 1; tt >= 0; --tt) {
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    float g = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < K; ++j) g = fmaf(P[k][j], s_b[tt][tid][j], g);
+                    const uint16_t hi = to_bf16(g);
+                    s_hi[tid * K + k][tt] = hi;
+                    s_lo[tid * K + k][tt] = to_bf16(g - from_bf16(hi));
+                }
+                float N[K][K];
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int j = 0; j < K; ++j) {
+                        float v = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < K; ++q) v = fmaf(P[k][q], s_A[tt][tid][q * K + j], v);
+                        N[k][j] = v;
+                    }
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int j = 0; j < K; ++j) P[k][j] = N[k][j];
+            }
+        }
+        __syncthreads();
+        // carry += (g x)[rows][tokens] . s[tokens][m]
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const int t = wave + 4 * q;
+            if (t < TILES) {
+                const int rt = t % 2, ct = t / 2;
+                const int kk = 8 * (lane >> 5);
+                const bf16x8 B = operand(&s_wT[32 * ct + (lane & 31)][kk]);
+                acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(operand(&s_hi[32 * rt + (lane & 31)][kk]), B,
+                                                                 acc[q], 0, 0, 0);
+                acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(operand(&s_lo[32 * rt + (lane & 31)][kk]), B,
+                                                                 acc[q], 0, 0, 0);
+            }
+        }
+    }
+    // carry rows (c, k) and Phi = P
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) {
+        const int t = wave + 4 * q;
+        if (t < TILES) {
+            const int rt = t % 2, ct = t / 2;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = 32 * rt + drow(lane, i), m = 32 * ct + (lane & 31);
+                const int c = c0 + r / K, k = r % K;
+                if (c < a.C) {
+                    const long long plane = ((long long)b * a.chunks + chunk_index) * a.C + c;
+                    a.carry[(plane * K + k) * M + m] = acc[q][i];
+                }
+            }
+        }
+    }
+    if (tid < G && c0 + tid < a.C) {
+        const long long plane = ((long long)b * a.chunks + chunk_index) * a.C + c0 + tid;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int j = 0; j < K; ++j) a.phi[(plane * K + k) * K + j] = P[k][j];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // combine: the state entering every chunk, serial over the chunks of one (b, c, m)
 // ---------------------------------------------------------------------------------------------
 template <int K>
@@ -360,9 +549,22 @@ int launch_typed(LatticeArgs &a, hipStream_t stream) {
     constexpr int G = BLOCK / L;
     const long long groups = (a.C + G - 1) / G;
     if (a.chunks > 1) {
-        const long long blocks = (long long)a.B * (a.chunks - 1) * groups;
-        hipLaunchKernelGGL((lattice_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
-        if (int rc = check_launch("lattice_summary")) return rc;
+        // the summary: on the matrix cores for bf16 at K <= 4, M >= 32 and 16-token chunks
+        bool summarised = false;
+        if constexpr (std::is_same<IO, bf16_t>::value && K <= 4 && M >= 32) {
+            if (a.chunk % summary_mfma::TT == 0) {
+                constexpr int GM = summary_mfma::ROWS / K;
+                const long long blocks = (long long)a.B * (a.chunks - 1) * ((a.C + GM - 1) / GM);
+                hipLaunchKernelGGL((lattice_summary_mfma<K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+                if (int rc = check_launch("lattice_summary_mfma")) return rc;
+                summarised = true;
+            }
+        }
+        if (!summarised) {
+            const long long blocks = (long long)a.B * (a.chunks - 1) * groups;
+            hipLaunchKernelGGL((lattice_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+            if (int rc = check_launch("lattice_summary")) return rc;
+        }
         const long long threads = (long long)a.B * a.C * M;
         hipLaunchKernelGGL((lattice_combine<K>), dim3((threads + BLOCK - 1) / BLOCK), dim3(BLOCK),
                            0, stream, a);

@@ -261,3 +261,22 @@ def test_mixer_prefill_then_decode(torch_mod, plugin):
     streamed = torch.cat(parts, dim=1)
     assert max_abs(to_numpy(streamed), to_numpy(full)) <= 2e-5
     assert len(cache) == 21
+
+
+@pytest.mark.parametrize("order,memory", [(1, 64), (2, 64), (4, 32), (2, 128)])
+@pytest.mark.parametrize("chunk", [32, 48, 40])
+def test_bf16_chunk_summaries(torch_mod, plugin, order, memory, chunk):
+    """bf16 with several chunks: 16-token multiples take the matrix-core summary (backward scan of
+    the stage maps + a GEMM of the injections with s), 40 takes the per-slot summary; both
+    against the fp32 oracle on the bf16-rounded inputs, with a mask, a carried-in state and a
+    partial channel group."""
+    rng = np.random.default_rng(40 + order + memory + chunk)
+    values = L.random_inputs(rng, 2, 200, 70, order, memory)
+    state = (rng.standard_normal((2, order, 70, memory)) * 0.1).astype(np.float32)
+    valid = rng.random((2, 200)) > 0.15
+    y, final = _run(plugin, torch_mod, values, valid, state, "cauchy_x_hyperbolic", "bfloat16",
+                    chunk=chunk)
+    want_y, want_state = _oracle(values, valid, state, "cauchy_x_hyperbolic", "bfloat16", torch_mod)
+    _assert(y, want_y, "bfloat16", f"chunk {chunk} output")
+    # the state stays float32 through both summaries (the GEMM's left operand is split hi + lo)
+    assert max_abs(final, want_state) <= 1e-4, f"chunk {chunk} state: {max_abs(final, want_state):.3e}"
