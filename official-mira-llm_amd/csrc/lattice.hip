@@ -238,6 +238,9 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     constexpr int CT = M / 32;                   // output column tiles
     constexpr int TILES = 2 * CT;                // 32 x 32 output tiles (2 row tiles)
     constexpr int PER_WAVE = (TILES + 3) / 4;
+    constexpr int PAIRS = TT * G / BLOCK;        // (token, channel) pairs per thread per tile
+    constexpr int WPT = TT * M / BLOCK;          // s elements per thread per tile
+    static_assert(PAIRS >= 1 && TT * G % BLOCK == 0 && WPT >= 1 && TT * M % BLOCK == 0, "tile shape");
     const int groups = (a.C + G - 1) / G;
     const int summarised = a.chunks - 1;
     int block = blockIdx.x;
@@ -249,39 +252,50 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     const int c0 = group * G;
     const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
 
-    __shared__ float s_A[TT][G][K * K];          // per (token, channel): A_t, row-major [k][j]
-    __shared__ float s_b[TT][G][K];              // b_t scaled by x_t (the injection of U = s)
+    __shared__ float s_A[TT][K * K][G];          // per token: A_t, [k][j] entries over channels
+    __shared__ float s_b[TT][K][G];              // b_t scaled by x_t (the injection of U = s)
     __shared__ alignas(16) uint16_t s_wT[M][TP]; // s^T of the tile, [m][token]
     __shared__ alignas(16) uint16_t s_hi[ROWS][TP], s_lo[ROWS][TP];   // g x, [(c, k)][token]
 
-    f32x16 acc[PER_WAVE];
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) acc[q] = f32x16{};
-    // the backward product P = A_L .. A_(s+1), one thread per channel
-    float P[K][K];
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int j = 0; j < K; ++j) P[k][j] = k == j ? 1.0f : 0.0f;
-
-    const int first = chunk_index * a.chunk;
+    // raw inputs of one tile, loaded a tile ahead: per pair alpha[K], beta[K], x; s elements
+    struct Raw { uint16_t al[PAIRS][K], be[PAIRS][K], x[PAIRS], w[WPT]; bool on[PAIRS]; };
+    const bf16_t *alpha_p = static_cast<const bf16_t *>(a.alpha);
+    const bf16_t *beta_p = static_cast<const bf16_t *>(a.beta);
+    const uint16_t *x_p = static_cast<const uint16_t *>(a.x);
     const uint16_t *write = static_cast<const uint16_t *>(a.write);
-    for (int tile = first + a.chunk - TT; tile >= first; tile -= TT) {
-        __syncthreads();                                       // previous tile's operands used
-        // stage maps of the tile as an affine map of (V, U): push the K basis states and U = 1
-        for (int i = tid; i < TT * G; i += BLOCK) {
-            const int tt = i / G, cl = i % G, c = c0 + cl;
+    auto fetch = [&](Raw &r, int tile) {
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p) {
+            const int i = tid + p * BLOCK, tt = i / G, c = c0 + i % G;
             const long long row = (long long)b * a.T + tile + tt;
+            r.on[p] = c < a.C && (!a.valid || a.valid[row]);
+            const long long cc = c < a.C ? c : 0;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                r.al[p][k] = alpha_p[row * a.alpha_row + cc * K + k].bits;
+                r.be[p][k] = beta_p[row * a.beta_row + cc * K + k].bits;
+            }
+            r.x[p] = x_p[row * a.x_row + cc];
+        }
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int i = tid + q * BLOCK, tt = i / M, m = i % M;
+            r.w[q] = write[((long long)b * a.T + tile + tt) * M + m];
+        }
+    };
+    // stage maps of a tile as an affine map of (V, U): push the K basis states and U = 1
+    auto stage = [&](const Raw &r) {
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p) {
+            const int i = tid + p * BLOCK, tt = i / G, cl = i % G;
             float Acol[K][K], bv[K];
-            const bool on = c < a.C && (!a.valid || a.valid[row]);
-            if (on) {
+            if (r.on[p]) {
                 float rc[K], rs[K];
-                const bf16_t *alpha = static_cast<const bf16_t *>(a.alpha) + row * a.alpha_row + (long long)c * K;
-                const bf16_t *beta = static_cast<const bf16_t *>(a.beta) + row * a.beta_row + (long long)c * K;
 #pragma unroll
                 for (int k = 0; k < K; ++k)
-                    stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc[k], rs[k]);
-                const float xv = load(static_cast<const bf16_t *>(a.x) + row * a.x_row + c);
+                    stage_coefficients(from_bf16(r.al[p][k]), from_bf16(r.be[p][k]), radius_kind,
+                                       rotation_kind, rc[k], rs[k]);
+                const float xv = from_bf16(r.x[p]);
 #pragma unroll
                 for (int col = 0; col <= K; ++col) {           // col < K: basis state e_col; K: U = 1
                     float V[K];
@@ -302,7 +316,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
                         else bv[k] = V[k] * xv;
                     }
                 }
-            } else {
+            } else {                                           // masked or past C: V unchanged
 #pragma unroll
                 for (int k = 0; k < K; ++k) {
 #pragma unroll
@@ -313,25 +327,53 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
 #pragma unroll
             for (int k = 0; k < K; ++k) {
 #pragma unroll
-                for (int j = 0; j < K; ++j) s_A[tt][cl][k * K + j] = Acol[k][j];
-                s_b[tt][cl][k] = bv[k];
+                for (int j = 0; j < K; ++j) s_A[tt][k * K + j][cl] = Acol[k][j];
+                s_b[tt][k][cl] = bv[k];
             }
         }
-        // s of the tile, transposed: [m][token]
-        for (int i = tid; i < TT * M; i += BLOCK) {
-            const int tt = i / M, m = i % M;
-            s_wT[m][tt] = write[((long long)b * a.T + tile + tt) * M + m];
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int i = tid + q * BLOCK, tt = i / M, m = i % M;
+            s_wT[m][tt] = r.w[q];
         }
+    };
+
+    f32x16 acc[PER_WAVE];
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) acc[q] = f32x16{};
+    // the backward product P = A_L .. A_(s+1), one thread per channel
+    float P[K][K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int j = 0; j < K; ++j) P[k][j] = k == j ? 1.0f : 0.0f;
+
+    const int first = chunk_index * a.chunk;
+    const int last_tile = first + a.chunk - TT;
+    Raw cur, next;
+    fetch(cur, last_tile);
+    for (int tile = last_tile; tile >= first; tile -= TT) {
+        __syncthreads();                                       // previous tile's operands used
+        stage(cur);
+        if (tile - TT >= first) fetch(next, tile - TT);        // in flight during the scan
         __syncthreads();
-        // backward scan: g_s = P b_s x_s, then P = P A_s
+        // backward scan over the tile, maps read into registers first: g_s = P b_s x_s, P = P A_s
         if (tid < G) {
-#pragma unroll 4
+            float At[TT][K * K], bt[TT][K];
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+                for (int q = 0; q < K * K; ++q) At[tt][q] = s_A[tt][q][tid];
+#pragma unroll
+                for (int k = 0; k < K; ++k) bt[tt][k] = s_b[tt][k][tid];
+            }
+#pragma unroll
             for (int tt = TT - 1; tt >= 0; --tt) {
 #pragma unroll
                 for (int k = 0; k < K; ++k) {
                     float g = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < K; ++j) g = fmaf(P[k][j], s_b[tt][tid][j], g);
+                    for (int j = 0; j < K; ++j) g = fmaf(P[k][j], bt[tt][j], g);
                     const uint16_t hi = to_bf16(g);
                     s_hi[tid * K + k][tt] = hi;
                     s_lo[tid * K + k][tt] = to_bf16(g - from_bf16(hi));
@@ -343,7 +385,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
                     for (int j = 0; j < K; ++j) {
                         float v = 0.0f;
 #pragma unroll
-                        for (int q = 0; q < K; ++q) v = fmaf(P[k][q], s_A[tt][tid][q * K + j], v);
+                        for (int q = 0; q < K; ++q) v = fmaf(P[k][q], At[tt][q * K + j], v);
                         N[k][j] = v;
                     }
 #pragma unroll
@@ -367,6 +409,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
                                                                  acc[q], 0, 0, 0);
             }
         }
+        cur = next;
     }
     // carry rows (c, k) and Phi = P
 #pragma unroll

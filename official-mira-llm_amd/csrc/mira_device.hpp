@@ -47,7 +47,8 @@ __device__ __forceinline__ float load(const IO *p) { return to_float(*p); }
 // The arch code is the reference kernel's stage mode (kernel/cuda/mira_dspv2/mira.py:305-309):
 // 3 cauchy_x_mobius, 6 cauchy_x_hyperbolic, 7 cauchy_x_identity, then for 8..19 radius
 // (mode-8)/3+1 in {gaussian, expexp, expsoftplus, hill} and rotation (mode-8)%3 in
-// {mobius, hyperbolic, identity}. Accurate libm functions are used (no fast-math intrinsics).
+// {mobius, hyperbolic, identity}. Reciprocals and exponentials come from the hardware
+// approximations refined to a few ulp (rcp_refined, exp_refined); the identity rotation uses sincosf.
 // ---------------------------------------------------------------------------------------------
 enum Radius { CAUCHY = 0, GAUSSIAN = 1, EXPEXP = 2, EXPSOFTPLUS = 3, HILL = 4 };
 enum Rotation { MOBIUS = 0, HYPERBOLIC = 1, IDENTITY = 2 };
@@ -62,6 +63,22 @@ __host__ __device__ __forceinline__ int rotation_of(int mode) {
     return mode == 3 ? MOBIUS : (mode == 6 ? HYPERBOLIC : (mode == 7 ? IDENTITY : (mode - 8) % 3));
 }
 
+// Reciprocal, quotient and exponential from the hardware approximations (v_rcp_f32, v_exp_f32)
+// refined to within a few ulp: one Newton step for the reciprocal (r' = r + r (1 - d r)), one
+// residual correction for the quotient, and Cody-Waite range reduction for e^x
+// (x = k ln2 + f, ln2 split in a high part exact in float and a low part; e^x = 2^k 2^(f/ln2)).
+__device__ __forceinline__ float rcp_refined(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    return fmaf(r, fmaf(-d, r, 1.0f), r);
+}
+__device__ __forceinline__ float exp_refined(float x) {
+    x = fminf(fmaxf(x, -104.0f), 88.7f);             // e^x is 0 / +inf beyond these in float
+    const float k = rintf(x * 1.44269504088896341f);
+    float f = fmaf(-k, 0.693145751953125f, x);       // ln2 high part: 11 significant bits
+    f = fmaf(-k, 1.42860682030941723212e-6f, f);     // ln2 - high part
+    return ldexpf(__builtin_amdgcn_exp2f(f * 1.44269504088896341f), (int)k);
+}
+
 // r cos(theta) and r sin(theta) of one stage.
 __device__ __forceinline__ void stage_coefficients(float alpha, float beta, int radius_kind,
                                                    int rotation_kind, float &rc, float &rs) {
@@ -69,31 +86,33 @@ __device__ __forceinline__ void stage_coefficients(float alpha, float beta, int 
     if (rotation_kind == MOBIUS) {
         // sin = (1 - a^2)/(1 + a^2), cos = 2a/(1 + a^2), written in 1/a above |a| = 1
         const bool small = fabsf(alpha) <= 1.0f;
-        const float base = small ? alpha : 1.0f / alpha;
+        const float base = small ? alpha : rcp_refined(alpha);
         const float square = base * base;
-        const float denominator = 1.0f + square;
-        c = 2.0f * base / denominator;
-        s = (small ? (1.0f - square) : (square - 1.0f)) / denominator;
+        const float inv = rcp_refined(1.0f + square);
+        c = 2.0f * base * inv;
+        s = (small ? (1.0f - square) : (square - 1.0f)) * inv;
     } else if (rotation_kind == HYPERBOLIC) {
-        // cos = sech(a) = 2e/(1 + e^2) with e = exp(-|a|), sin = tanh(a)
-        const float e = expf(-fabsf(alpha));
-        c = 2.0f * e / (1.0f + e * e);
-        s = tanhf(alpha);
+        // with e = exp(-|a|): cos = sech(a) = 2e/(1 + e^2), sin = tanh(a) = sign(a) (1 - e^2)/(1 + e^2)
+        const float e = exp_refined(-fabsf(alpha));
+        const float inv = rcp_refined(fmaf(e, e, 1.0f));
+        c = 2.0f * e * inv;
+        s = copysignf(fmaf(-e, e, 1.0f) * inv, alpha);
     } else {
         sincosf(alpha, &s, &c);
     }
     float r;
     if (radius_kind == CAUCHY) {
-        r = 1.0f / (1.0f + beta * beta);
+        r = rcp_refined(fmaf(beta, beta, 1.0f));
     } else if (radius_kind == GAUSSIAN) {
-        r = expf(-(beta * beta));
+        r = exp_refined(-(beta * beta));
     } else if (radius_kind == EXPEXP) {
-        r = expf(-expf(fminf(beta, 80.0f)));
+        r = exp_refined(-exp_refined(fminf(beta, 80.0f)));
     } else if (radius_kind == EXPSOFTPLUS) {
-        r = 1.0f / (1.0f + expf(beta));            // exp(-softplus(beta)) = sigmoid(-beta)
+        r = rcp_refined(1.0f + exp_refined(beta));   // exp(-softplus(beta)) = sigmoid(-beta)
     } else {
         const float q = beta * beta;                 // hill: q/(1+q), 1 - 1/(1+q) above q = 1
-        r = q > 1.0f ? 1.0f - 1.0f / (1.0f + q) : q / (1.0f + q);
+        const float inv = rcp_refined(1.0f + q);
+        r = q > 1.0f ? 1.0f - inv : q * inv;
     }
     rc = r * c;
     rs = r * s;

@@ -280,3 +280,35 @@ def test_bf16_chunk_summaries(torch_mod, plugin, order, memory, chunk):
     _assert(y, want_y, "bfloat16", f"chunk {chunk} output")
     # the state stays float32 through both summaries (the GEMM's left operand is split hi + lo)
     assert max_abs(final, want_state) <= 1e-4, f"chunk {chunk} state: {max_abs(final, want_state):.3e}"
+
+
+@pytest.mark.parametrize("arch", list(L.ARCH_STAGE))
+def test_stage_maps_against_fp64(torch_mod, plugin, arch):
+    """The kernel's stage maps alone, for 8192 (alpha, beta) pairs per arch over the ranges the
+    mixer feeds (|alpha| up to 12, beta up to 6): one decode step with K=1, x=0, state 1 reads
+    r cos(theta) out through the readout (nu = (0, 1), rho = (0, 1), gamma = 32: y = 32 r cos) and
+    -r sin(theta) as the new state. Against oracle/lattice.py's closed forms in float64."""
+    torch = torch_mod
+    rng = np.random.default_rng(99)
+    C = 8192
+    alpha = np.concatenate([rng.uniform(-12, 12, C // 2), rng.normal(0, 0.05, C // 2)]).astype(np.float32)
+    beta = np.concatenate([rng.uniform(-6, 6, C // 2), rng.normal(0, 0.05, C // 2)]).astype(np.float32)
+    x = np.zeros((1, 1, C), np.float32)
+    rho = np.zeros((1, 1, C, 2), np.float32)
+    rho[..., 1] = 1.0
+    gamma = np.full((1, 1, C), 32.0, np.float32)
+    write = np.ones((1, 1, 1), np.float32)
+    read = np.zeros((1, 1, 2, 1), np.float32)
+    read[:, :, 1, 0] = 1.0
+    state = np.ones((1, 1, C, 1), np.float32)
+    ins = [to_device(v) for v in (x, alpha.reshape(1, 1, C, 1), rho, gamma, write, read,
+                                  beta.reshape(1, 1, C, 1))]
+    out, final = plugin.matrix_lattice_step(*ins, to_device(state), arch=arch)
+    torch.cuda.synchronize()
+    rotation, radius = L.stage_maps(arch)
+    cos, sin = rotation(alpha.astype(np.float64))
+    r = radius(beta.astype(np.float64))
+    got_rc = to_numpy(out).reshape(C) / 32.0
+    got_rs = -to_numpy(final).reshape(C)
+    assert max_abs(got_rc, r * cos) <= 1e-6, f"r cos: {max_abs(got_rc, r * cos):.3e}"
+    assert max_abs(got_rs, r * sin) <= 1e-6, f"r sin: {max_abs(got_rs, r * sin):.3e}"
