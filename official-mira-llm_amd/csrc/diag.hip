@@ -615,6 +615,251 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
     *reinterpret_cast<float4 *>(hstate + at) = make_float4(h[0], h[1], h[2], h[3]);
 }
 
+// ---------------------------------------------------------------------------------------------
+// column prefill: one workgroup per (sequence, 64-channel column), all T tokens in order
+// ---------------------------------------------------------------------------------------------
+constexpr int COL_C = 64;                        // channels per column
+constexpr int COL_WAVES = 16;
+constexpr int COL_SEG = 4;                       // tokens per segment (half a wave)
+constexpr int COL_SEGS = 2 * COL_WAVES;          // segments per tile
+constexpr int COL_TILE = COL_SEGS * COL_SEG;     // tokens per tile
+// tiles whose loads are in flight ahead of use: two of a 16-bit type, one of float32 (whose
+// packs are twice the registers)
+__host__ __device__ constexpr int col_ahead(int element_bytes) { return element_bytes == 4 ? 1 : 2; }
+constexpr int COL_FOLD = 8;                      // maps the folding wave reads per LDS round
+
+// two channels of one token: a dword of a 16-bit type, two of float32
+template <typename IO> struct Duo { typedef unsigned type; };
+template <> struct Duo<float> { typedef u32x2 type; };
+
+template <typename IO, int POLICY = 0>
+__device__ __forceinline__ typename Duo<IO>::type load_duo(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    if constexpr (sizeof(IO) == 4) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POLICY);
+    else return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POLICY);
+}
+template <typename IO, int POLICY = 0>
+__device__ __forceinline__ void store_duo(__amdgpu_buffer_rsrc_t r, unsigned off,
+                                          const typename Duo<IO>::type &v) {
+    if constexpr (sizeof(IO) == 4) __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, POLICY);
+    else __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, POLICY);
+}
+template <typename IO>
+__device__ __forceinline__ void unpack_duo(const typename Duo<IO>::type &p, float (&f)[2]) {
+    if constexpr (sizeof(IO) == 4) { f[0] = __uint_as_float(p[0]); f[1] = __uint_as_float(p[1]); }
+    else { f[0] = low_half(p, IO{}); f[1] = high_half(p, IO{}); }
+}
+template <typename IO>
+__device__ __forceinline__ typename Duo<IO>::type pack_duo(const float (&f)[2]) {
+    if constexpr (sizeof(IO) == 4) {
+        return u32x2{__float_as_uint(f[0]), __float_as_uint(f[1])};
+    } else if constexpr (__is_same(IO, bf16_t)) {
+        return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2{f[0], f[1]}), bf16x2));
+    } else {
+        return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2{f[0], f[1]}), f16x2));
+    }
+}
+
+// THE COLUMN FORM. Where the batch has enough 64-channel columns to give every CU one, a
+// workgroup scans its column over all T tokens and no state crosses workgroups. A tile is 128
+// tokens: 16 waves x 2 half-wave segments of 4 tokens; a lane holds 2 channels of its segment.
+// Step i issues the loads of tile i+2, computes tile i's conv inputs b = (1-a)u and each
+// segment's map (A, H) (kept: a and b in registers, the map in LDS), and after one barrier
+// wave 0 folds the 32 maps of tile i in token order from the state entering the tile, writing
+// each segment's entering state to LDS and carrying the state on to tile i+1, while every wave
+// replays tile i-1 (h = a h + b) from the entering states folded in step i-1 and stores y.
+template <typename IO, int W>
+__global__ __launch_bounds__(COL_WAVES * 64) void diag_column_kernel(DiagArgs a) {
+    constexpr int H = W - 1;                     // conv history
+    typedef typename Duo<IO>::type DuoT;
+    constexpr int AHEAD = col_ahead(sizeof(IO));
+    __shared__ alignas(16) float2 s_map[2][COL_SEGS][COL_C];    // each segment's map (A, H), per channel
+    __shared__ alignas(16) float s_enter[2][COL_SEGS][COL_C];   // each segment's entering state
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int seg = 2 * wave + (lane >> 5), pair = lane & 31;
+    const int columns = (a.D + COL_C - 1) / COL_C;
+    const int b = blockIdx.x / columns, c0 = (blockIdx.x % columns) * COL_C;
+    const int d = c0 + 2 * pair;                 // this lane's channels d, d + 1 (D is even)
+    const bool dact = d < a.D;
+    const int tiles = (a.T + COL_TILE - 1) / COL_TILE;
+    const long long row0 = (long long)b * a.T;
+    const unsigned seq_bytes = (unsigned)a.T * (unsigned)a.D * (unsigned)sizeof(IO);
+    const IO *x = static_cast<const IO *>(a.x);
+    const __amdgpu_buffer_rsrc_t xr = resource(x + row0 * a.D, seq_bytes);
+    const __amdgpu_buffer_rsrc_t ar = resource(static_cast<const IO *>(a.a) + row0 * a.D, seq_bytes);
+    const __amdgpu_buffer_rsrc_t yr = resource(static_cast<IO *>(a.y) + row0 * a.D, seq_bytes);
+    // Offsets need no range checks: a token at or past T, or before 0 (the 32-bit offset wraps),
+    // lies outside the sequence's buffer resource, whose loads read zero and whose stores are
+    // dropped; a lane past D starts at OUT_OF_RANGE, and OUT_OF_RANGE + T D bytes < 2^32.
+    // offset(tile, k): token tile * COL_TILE + seg * COL_SEG + k (k may be negative); the
+    // tile- and k-dependent part is uniform, so each offset is one add to the lane's base.
+    const unsigned row_bytes = (unsigned)a.D * (unsigned)sizeof(IO);
+    const unsigned lane_base = (dact ? (unsigned)d * (unsigned)sizeof(IO) : OUT_OF_RANGE)
+                             + (unsigned)(seg * COL_SEG) * row_bytes;
+    auto offset = [&](int tile, int k) -> unsigned {
+        return lane_base + (unsigned)(tile * COL_TILE + k) * row_bytes;
+    };
+    float wv[2][W], bias[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) wv[e][j] = dact ? a.w[(long long)(d + e) * W + j] : 0.0f;
+        bias[e] = (dact && a.bias) ? a.bias[d + e] : 0.0f;
+    }
+    // the lane, tile and token holding token T - 1 (for the final state)
+    const int last_tile = (a.T - 1) / COL_TILE, last_k = (a.T - 1) % COL_SEG;
+    const bool holds_last = dact && seg == ((a.T - 1) % COL_TILE) / COL_SEG;
+
+    // raw packs of one tile (x, a and the H x before the segment), loaded AHEAD tiles ahead
+    struct Packs { DuoT x[COL_SEG], a[COL_SEG], h[H]; };
+    // a tile's decay factors and conv inputs, kept from its summary to its replay
+    struct Kept { float a[COL_SEG][2], b[COL_SEG][2]; };
+    // the packs of a tile; `first` for tile 0, whose history may come from the ring
+    auto fetch = [&](Packs &p, int tile, bool first) {
+        const int t0 = tile * COL_TILE + seg * COL_SEG;
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+            const int tt = t0 - H + j;
+            if (!first || tt >= 0 || !a.ring_in) {
+                p.h[j] = load_duo<IO>(xr, offset(tile, j - H));
+            } else {                             // before this call's first token: the ring
+                float f[2] = {0.0f, 0.0f};
+                const long long stream = a.pos + tt;
+                if (dact && stream >= 0) {
+                    const IO *ring = static_cast<const IO *>(a.ring_in);
+                    const int s = (int)(stream % H);
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) f[e] = load(ring + ((long long)b * a.D + d + e) * H + s);
+                }
+                p.h[j] = pack_duo<IO>(f);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < COL_SEG; ++k) {
+            const unsigned off = offset(tile, k);
+            p.x[k] = load_duo<IO>(xr, off);
+            p.a[k] = load_duo<IO>(ar, off);
+        }
+    };
+    // conv and decay inputs of a segment from zero state, and the segment's map
+    auto summarise = [&](const Packs &p, Kept &kept, int ring) {
+        float win[H][2];
+#pragma unroll
+        for (int j = 0; j < H; ++j) unpack_duo<IO>(p.h[j], win[j]);
+        float A[2] = {1.0f, 1.0f}, Hs[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < COL_SEG; ++k) {
+            float xf[2], af[2];
+            unpack_duo<IO>(p.x[k], xf);
+            unpack_duo<IO>(p.a[k], af);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                float u = bias[e];
+#pragma unroll
+                for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], win[j][e], u);
+                u = fmaf(wv[e][H], xf[e], u);
+                const float bv = fmaf(-af[e], u, u);
+                kept.a[k][e] = af[e];
+                kept.b[k][e] = bv;
+                Hs[e] = fmaf(af[e], Hs[e], bv);
+                A[e] *= af[e];
+#pragma unroll
+                for (int j = 0; j + 1 < H; ++j) win[j][e] = win[j + 1][e];
+                win[H - 1][e] = xf[e];
+            }
+        }
+        *reinterpret_cast<float4 *>(&s_map[ring][seg][2 * pair]) = make_float4(A[0], Hs[0], A[1], Hs[1]);
+    };
+    // wave 0, lane = channel: the entering state of every segment of a tile, in token order
+    float carry = (lane < COL_C && c0 + lane < a.D && a.h0 && wave == 0) ? a.h0[(long long)b * a.D + c0 + lane]
+                                                                        : 0.0f;
+    auto fold = [&](int ring) {
+#pragma unroll
+        for (int s0 = 0; s0 < COL_SEGS; s0 += COL_FOLD) {
+            float2 m[COL_FOLD];
+#pragma unroll
+            for (int s = 0; s < COL_FOLD; ++s) m[s] = s_map[ring][s0 + s][lane];
+#pragma unroll
+            for (int s = 0; s < COL_FOLD; ++s) {
+                s_enter[ring][s0 + s][lane] = carry;
+                carry = fmaf(m[s].x, carry, m[s].y);
+            }
+        }
+    };
+    auto replay = [&](int tile, const Kept &kept, int ring) {
+        const float2 enter = *reinterpret_cast<const float2 *>(&s_enter[ring][seg][2 * pair]);
+        float h[2] = {enter.x, enter.y};
+#pragma unroll
+        for (int k = 0; k < COL_SEG; ++k) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) h[e] = fmaf(kept.a[k][e], h[e], kept.b[k][e]);
+            store_duo<IO, NT>(yr, offset(tile, k), pack_duo<IO>(h));
+            if (tile == last_tile && k == last_k && holds_last && a.hT) {
+                a.hT[(long long)b * a.D + d] = h[0];
+                a.hT[(long long)b * a.D + d + 1] = h[1];
+            }
+        }
+    };
+
+    // step i: loads of tile i + AHEAD, summary of tile i, barrier, fold of tile i (wave 0),
+    // replay of tile i - 1. AHEAD + 1 pack sets and 2 kept sets rotate through unrolled steps.
+    auto step = [&](int i, Packs &cur, Packs &ahead, Kept &now, Kept &before) {
+        fetch(ahead, i + AHEAD, false);
+        if (i < tiles) summarise(cur, now, i & 1);
+        lds_barrier();
+        if (wave == 0 && i < tiles) fold(i & 1);
+        if (i >= 1) replay(i - 1, before, (i - 1) & 1);
+    };
+    Kept k0, k1;
+    if constexpr (AHEAD == 2) {
+        Packs p0, p1, p2;
+        fetch(p0, 0, true);
+        fetch(p1, 1, false);
+        for (int i = 0; i <= tiles; i += 6) {
+            step(i, p0, p2, k0, k1);
+            if (i + 1 > tiles) break;
+            step(i + 1, p1, p0, k1, k0);
+            if (i + 2 > tiles) break;
+            step(i + 2, p2, p1, k0, k1);
+            if (i + 3 > tiles) break;
+            step(i + 3, p0, p2, k1, k0);
+            if (i + 4 > tiles) break;
+            step(i + 4, p1, p0, k0, k1);
+            if (i + 5 > tiles) break;
+            step(i + 5, p2, p1, k1, k0);
+        }
+    } else {
+        static_assert(AHEAD == 1, "one or two tiles ahead");
+        Packs p0, p1;
+        fetch(p0, 0, true);
+        for (int i = 0; i <= tiles; i += 2) {
+            step(i, p0, p1, k0, k1);
+            if (i + 1 > tiles) break;
+            step(i + 1, p1, p0, k1, k0);
+        }
+    }
+
+    // the ring after this call: the last H stream tokens, each in slot (stream mod H)
+    if (a.ring_out && wave == 0 && lane < 32 && dact) {
+        const IO *ring_in = static_cast<const IO *>(a.ring_in);
+        IO *ring_out = static_cast<IO *>(a.ring_out);
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+            const long long stream = a.pos + a.T - H + j;
+            const long long t = a.T - H + j;
+            const int s = (int)(((stream % H) + H) % H);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const long long at = ((long long)b * a.D + d + e) * H + s;
+                if (stream < 0) ring_out[at] = from_float<IO>(0.0f);
+                else if (t >= 0) ring_out[at] = x[(row0 + t) * a.D + d + e];
+                else if (!ring_in) ring_out[at] = from_float<IO>(0.0f);
+                else if (ring_in != ring_out) ring_out[at] = ring_in[at];
+            }
+        }
+    }
+}
+
 std::atomic<unsigned> g_epoch{0};
 
 // compute units of the current device (cached per device)
@@ -638,6 +883,14 @@ int scan_typed(const DiagArgs &a, void *ws, size_t bytes, hipStream_t stream) {
     if (bytes < lay.total) return fail(MIRA_ERR_ARG, "diag: workspace too small");
     if ((unsigned long long)a.T * a.D * sizeof(IO) >= OUT_OF_RANGE)
         return fail(MIRA_DECLINE, "diag: one sequence must hold under 2 GiB of x");
+    // the column form wherever the batch has a 64-channel column for at least half the CUs
+    // (its offsets run to T + 4 tiles of rows past the sequence start and must not wrap)
+    const long long columns = (long long)a.B * ((a.D + COL_C - 1) / COL_C);
+    const bool offsets_fit = ((unsigned long long)a.T + 4 * COL_TILE) * a.D * sizeof(IO) < OUT_OF_RANGE;
+    if (2 * columns >= compute_units() && offsets_fit) {
+        hipLaunchKernelGGL((diag_column_kernel<IO, 4>), dim3(columns), dim3(COL_WAVES * 64), 0, stream, a);
+        return check_launch("diag_column");
+    }
     unsigned epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
     if (epoch == 0) epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
     // persistent workgroups: one per CU in all, spread evenly over the chains

@@ -84,6 +84,51 @@ def test_shapes_and_dtypes(torch_mod, plugin, dtype, B, T, D):
     assert max_abs(to_numpy(hT), h_last) <= (FP32_ABS if dtype == "float32" else 1e-3)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("B,T,D", [(2, 333, 4096), (128, 130, 64), (3, 257, 2900), (64, 1, 128)])
+def test_column_form_shapes(torch_mod, plugin, dtype, B, T, D):
+    """Batches with at least 128 columns of 64 channels (the column form on a 256-CU part):
+    ragged token tails, a partial last column (2900 = 45 x 64 + 20), T = 1, bias and h0."""
+    torch = torch_mod
+    rng = np.random.default_rng(B * 7 + T * 3 + D)
+    x, a, w, bias, h0 = Bl.diag_inputs(rng, B, T, D, h0_scale=0.1)
+    bias = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    td = getattr(torch, dtype)
+    y, hT, _ = plugin.diag_conv_scan(to_device(x, td), to_device(a, td), to_device(w),
+                                     to_device(bias), h0=to_device(h0), return_state=True)
+    h, h_last, _ = Bl.diag_conv_scan(rounded(x, td), rounded(a, td), w, bias, h0)
+    _check(to_numpy(y), h, dtype, "y")
+    assert max_abs(to_numpy(hT), h_last) <= (FP32_ABS if dtype == "float32" else 1e-3)
+    assert plugin.diag_workspace_error() == 0
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("T1,T2", [(1, 2), (5, 300), (128, 129)])
+def test_column_form_streaming_with_ring(torch_mod, plugin, dtype, T1, T2):
+    """The column form carrying h and the ring across calls (the second call updates the ring in
+    place) equals one call, and the ring holds the last three tokens."""
+    torch = torch_mod
+    td = getattr(torch, dtype)
+    rng = np.random.default_rng(T1 * 11 + T2)
+    B, D = 2, 4096
+    x, a, w, bias, h0 = Bl.diag_inputs(rng, B, T1 + T2, D, h0_scale=0.1)
+    X, A, W = to_device(x, td), to_device(a, td), to_device(w)
+    y_all, h_all, _ = plugin.diag_conv_scan(X, A, W, h0=to_device(h0), return_state=True)
+    ring = torch.zeros(B, D, 3, device="cuda", dtype=td)
+    y1, h1, ring = plugin.diag_conv_scan(X[:, :T1], A[:, :T1], W, h0=to_device(h0), ring=ring,
+                                         pos=0, return_state=True)
+    y2, h2, ring = plugin.diag_conv_scan(X[:, T1:], A[:, T1:], W, h0=h1, ring=ring, pos=T1,
+                                         return_state=True)
+    y_two = to_numpy(torch.cat([y1, y2], 1))
+    if dtype == "float32":
+        _check(y_two, to_numpy(y_all), dtype, "streamed y")
+    else:
+        assert scaled(y_two, to_numpy(y_all)) <= 1e-2
+    assert max_abs(to_numpy(h2), to_numpy(h_all)) <= 1e-5
+    want_ring = Bl.ring_after(rounded(x, td), np.zeros((B, D, 3), np.float32), 0)
+    assert np.array_equal(to_numpy(ring), want_ring), "ring after the stream"
+
+
 @pytest.mark.parametrize("T1,T2", [(1, 1), (2, 5), (64, 64), (100, 37), (3, 300)])
 def test_streaming_with_ring(torch_mod, plugin, T1, T2):
     """[0,T1) then [T1,T1+T2) carrying h and the ring equals one call."""
