@@ -209,14 +209,18 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
 // ---------------------------------------------------------------------------------------------
 // summary on the matrix cores (bf16 inputs): per channel the stage maps are affine in the state,
 // V_t = A_t V_(t-1) + b_t U_t with U_t = x_t s_t[m], and A_t, b_t (K x K, K) do not depend on m.
-// So the chunk's carry from a zero state is carry[k][m] = sum_s g_s[k] x_s s_s[m] with
-// g_s = A_L .. A_(s+1) b_s: a backward scan per channel gives g_s and Phi = A_L .. A_1 with
-// O(K^2) work per token instead of O(K M), and the sum over s is a GEMM,
-//     carry[(c, k)][m] = sum_s (g_s[c][k] x_s[c]) . s_s[m],
+// So the chunk's carry from a zero state is carry[k][m] = sum_s g_s[k] s_s[m] with
+// g_s = A_L .. A_(s+1) b_s x_s, and Phi = A_L .. A_1: O(K^2) work per token instead of O(K M),
+// and the sum over s is a GEMM,
+//     carry[(c, k)][m] = sum_s g_s[c][k] . s_s[m],
 // run on v_mfma_f32_32x32x16_bf16 with the left operand split into a bf16 high part and its
 // rounding remainder (float32-level accuracy; s is bf16 already).
 // A block owns 64 rows (c, k) -- 64 / K channels -- and walks the chunk backwards in tiles of 16
-// tokens: stage the tile's stage maps and s^T, scan it backwards, multiply-accumulate.
+// tokens. Every lane is one token of the tile: a 16-lane row holds the tile's tokens for 64 / (16 K)
+// channels, each lane computes its token's stage map, and the suffix products A_15 .. A_t of the
+// tile come from a four-round scan across the row (DPP row shifts; lanes past the row's end read
+// the identity). g_t = Pl A_15 .. A_(t+1) b_t x_t, where Pl is the product of the later tiles'
+// maps, which every lane of the row carries (the tile's product is lane 0's inclusive scan).
 // ---------------------------------------------------------------------------------------------
 namespace summary_mfma {
 constexpr int ROWS = 64, TT = 16, TP = TT + 8;
@@ -229,18 +233,48 @@ __device__ __forceinline__ bf16x8 operand(const uint16_t *p) {
 }
 __device__ __forceinline__ uint16_t to_bf16(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
 __device__ __forceinline__ float from_bf16(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// lane i of a 16-lane row takes lane i + N's value; past the row's end it keeps `fill`
+template <int N>
+__device__ __forceinline__ float from_row_above(float v, float fill) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill),
+                                                                 __builtin_bit_cast(int, v),
+                                                                 0x100 + N, 0xf, 0xf, false));
+}
+// X_t <- X_(t+N) X_t across the row (identity past its end): one round of the suffix scan
+template <int N, int K>
+__device__ __forceinline__ void suffix_round(float (&X)[K][K]) {
+    float Y[K][K], Z[K][K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int j = 0; j < K; ++j) Y[k][j] = from_row_above<N>(X[k][j], k == j ? 1.0f : 0.0f);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            float v = Y[k][0] * X[0][j];
+#pragma unroll
+            for (int q = 1; q < K; ++q) v = fmaf(Y[k][q], X[q][j], v);
+            Z[k][j] = v;
+        }
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int j = 0; j < K; ++j) X[k][j] = Z[k][j];
+}
 }  // namespace summary_mfma
 
 template <int K, int M>
 __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     using namespace summary_mfma;
     constexpr int G = ROWS / K;                  // channels per block
+    constexpr int CP = G / TT;                   // channels per lane (16 rows of 16 token lanes)
     constexpr int CT = M / 32;                   // output column tiles
     constexpr int TILES = 2 * CT;                // 32 x 32 output tiles (2 row tiles)
     constexpr int PER_WAVE = (TILES + 3) / 4;
-    constexpr int PAIRS = TT * G / BLOCK;        // (token, channel) pairs per thread per tile
     constexpr int WPT = TT * M / BLOCK;          // s elements per thread per tile
-    static_assert(PAIRS >= 1 && TT * G % BLOCK == 0 && WPT >= 1 && TT * M % BLOCK == 0, "tile shape");
+    static_assert(BLOCK == 256 && CP >= 1 && CP * TT == G && WPT >= 1 && TT * M % BLOCK == 0,
+                  "tile shape");
     const int groups = (a.C + G - 1) / G;
     const int summarised = a.chunks - 1;
     int block = blockIdx.x;
@@ -249,33 +283,31 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     const int chunk_index = block % summarised;
     const int b = block / summarised;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int c0 = group * G;
+    const int t = tid & (TT - 1), row = tid / TT;
+    const int c0 = group * G, cr = c0 + row * CP;    // this lane's first channel
     const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
 
-    __shared__ float s_A[TT][K * K][G];          // per token: A_t, [k][j] entries over channels
-    __shared__ float s_b[TT][K][G];              // b_t scaled by x_t (the injection of U = s)
-    __shared__ alignas(16) uint16_t s_wT[M][TP]; // s^T of the tile, [m][token]
-    __shared__ alignas(16) uint16_t s_hi[ROWS][TP], s_lo[ROWS][TP];   // g x, [(c, k)][token]
+    __shared__ alignas(16) uint16_t s_wT[M][TP];  // s^T of the tile, [m][token]
+    __shared__ alignas(16) uint16_t s_hi[ROWS][TP], s_lo[ROWS][TP];   // g, [(c, k)][token]
 
-    // raw inputs of one tile, loaded a tile ahead: per pair alpha[K], beta[K], x; s elements
-    struct Raw { uint16_t al[PAIRS][K], be[PAIRS][K], x[PAIRS], w[WPT]; bool on[PAIRS]; };
-    const bf16_t *alpha_p = static_cast<const bf16_t *>(a.alpha);
-    const bf16_t *beta_p = static_cast<const bf16_t *>(a.beta);
+    // raw inputs of this lane's token, loaded a tile ahead: alpha[K], beta[K], x per channel
+    struct Raw { uint16_t al[CP][K], be[CP][K], x[CP], w[WPT]; bool on; };
+    const uint16_t *alpha_p = static_cast<const uint16_t *>(a.alpha);
+    const uint16_t *beta_p = static_cast<const uint16_t *>(a.beta);
     const uint16_t *x_p = static_cast<const uint16_t *>(a.x);
     const uint16_t *write = static_cast<const uint16_t *>(a.write);
     auto fetch = [&](Raw &r, int tile) {
+        const long long rowi = (long long)b * a.T + tile + t;
+        r.on = !a.valid || a.valid[rowi];
 #pragma unroll
-        for (int p = 0; p < PAIRS; ++p) {
-            const int i = tid + p * BLOCK, tt = i / G, c = c0 + i % G;
-            const long long row = (long long)b * a.T + tile + tt;
-            r.on[p] = c < a.C && (!a.valid || a.valid[row]);
-            const long long cc = c < a.C ? c : 0;
+        for (int e = 0; e < CP; ++e) {
+            const long long cc = cr + e < a.C ? cr + e : 0;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-                r.al[p][k] = alpha_p[row * a.alpha_row + cc * K + k].bits;
-                r.be[p][k] = beta_p[row * a.beta_row + cc * K + k].bits;
+                r.al[e][k] = alpha_p[rowi * a.alpha_row + cc * K + k];
+                r.be[e][k] = beta_p[rowi * a.beta_row + cc * K + k];
             }
-            r.x[p] = x_p[row * a.x_row + cc];
+            r.x[e] = x_p[rowi * a.x_row + cc];
         }
 #pragma unroll
         for (int q = 0; q < WPT; ++q) {
@@ -283,19 +315,37 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
             r.w[q] = write[((long long)b * a.T + tile + tt) * M + m];
         }
     };
-    // stage maps of a tile as an affine map of (V, U): push the K basis states and U = 1
-    auto stage = [&](const Raw &r) {
+
+    f32x16 acc[PER_WAVE];
 #pragma unroll
-        for (int p = 0; p < PAIRS; ++p) {
-            const int i = tid + p * BLOCK, tt = i / G, cl = i % G;
-            float Acol[K][K], bv[K];
-            if (r.on[p]) {
+    for (int q = 0; q < PER_WAVE; ++q) acc[q] = f32x16{};
+    // Pl: the product of the maps of the tiles after the current one (per channel of the lane);
+    // after the last tile it is the chunk's Phi
+    float Pl[CP][K][K];
+#pragma unroll
+    for (int e = 0; e < CP; ++e)
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int j = 0; j < K; ++j) Pl[e][k][j] = k == j ? 1.0f : 0.0f;
+
+    const int first = chunk_index * a.chunk;
+    const int last_tile = first + a.chunk - TT;
+    Raw cur, next;
+    fetch(cur, last_tile);
+    for (int tile = last_tile; tile >= first; tile -= TT) {
+        __syncthreads();                                       // previous tile's operands used
+#pragma unroll
+        for (int e = 0; e < CP; ++e) {
+            // this token's stage map as an affine map of (V, U): A (K x K) and b, times x
+            float X[K][K], bx[K];
+            if (cur.on && cr + e < a.C) {
                 float rc[K], rs[K];
 #pragma unroll
                 for (int k = 0; k < K; ++k)
-                    stage_coefficients(from_bf16(r.al[p][k]), from_bf16(r.be[p][k]), radius_kind,
+                    stage_coefficients(from_bf16(cur.al[e][k]), from_bf16(cur.be[e][k]), radius_kind,
                                        rotation_kind, rc[k], rs[k]);
-                const float xv = from_bf16(r.x[p]);
+                const float xv = from_bf16(cur.x[e]);
 #pragma unroll
                 for (int col = 0; col <= K; ++col) {           // col < K: basis state e_col; K: U = 1
                     float V[K];
@@ -312,95 +362,75 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
                     V[0] = U;
 #pragma unroll
                     for (int k = 0; k < K; ++k) {
-                        if (col < K) Acol[k][col] = V[k];
-                        else bv[k] = V[k] * xv;
+                        if (col < K) X[k][col] = V[k];
+                        else bx[k] = V[k] * xv;
                     }
                 }
             } else {                                           // masked or past C: V unchanged
 #pragma unroll
                 for (int k = 0; k < K; ++k) {
 #pragma unroll
-                    for (int j = 0; j < K; ++j) Acol[k][j] = k == j ? 1.0f : 0.0f;
-                    bv[k] = 0.0f;
+                    for (int j = 0; j < K; ++j) X[k][j] = k == j ? 1.0f : 0.0f;
+                    bx[k] = 0.0f;
                 }
+            }
+            // inclusive suffix products across the row: X_t = A_15 .. A_t
+            suffix_round<1, K>(X);
+            suffix_round<2, K>(X);
+            suffix_round<4, K>(X);
+            suffix_round<8, K>(X);
+            // g_t = Pl A_15 .. A_(t+1) b_t x_t
+            float zb[K];
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                float v = 0.0f;
+#pragma unroll
+                for (int j = 0; j < K; ++j)
+                    v = fmaf(from_row_above<1>(X[k][j], k == j ? 1.0f : 0.0f), bx[j], v);
+                zb[k] = v;
             }
 #pragma unroll
             for (int k = 0; k < K; ++k) {
+                float g = 0.0f;
 #pragma unroll
-                for (int j = 0; j < K; ++j) s_A[tt][k * K + j][cl] = Acol[k][j];
-                s_b[tt][k][cl] = bv[k];
+                for (int j = 0; j < K; ++j) g = fmaf(Pl[e][k][j], zb[j], g);
+                const uint16_t hi = to_bf16(g);
+                s_hi[(row * CP + e) * K + k][t] = hi;
+                s_lo[(row * CP + e) * K + k][t] = to_bf16(g - from_bf16(hi));
             }
+            // Pl <- Pl (A_15 .. A_0), the tile's product from lane 0 of the row
+            float Tm[K][K], N[K][K];
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int j = 0; j < K; ++j) Tm[k][j] = __shfl(X[k][j], lane & ~(TT - 1));
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    float v = Pl[e][k][0] * Tm[0][j];
+#pragma unroll
+                    for (int q = 1; q < K; ++q) v = fmaf(Pl[e][k][q], Tm[q][j], v);
+                    N[k][j] = v;
+                }
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int j = 0; j < K; ++j) Pl[e][k][j] = N[k][j];
         }
 #pragma unroll
         for (int q = 0; q < WPT; ++q) {
             const int i = tid + q * BLOCK, tt = i / M, m = i % M;
-            s_wT[m][tt] = r.w[q];
+            s_wT[m][tt] = cur.w[q];
         }
-    };
-
-    f32x16 acc[PER_WAVE];
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) acc[q] = f32x16{};
-    // the backward product P = A_L .. A_(s+1), one thread per channel
-    float P[K][K];
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int j = 0; j < K; ++j) P[k][j] = k == j ? 1.0f : 0.0f;
-
-    const int first = chunk_index * a.chunk;
-    const int last_tile = first + a.chunk - TT;
-    Raw cur, next;
-    fetch(cur, last_tile);
-    for (int tile = last_tile; tile >= first; tile -= TT) {
-        __syncthreads();                                       // previous tile's operands used
-        stage(cur);
-        if (tile - TT >= first) fetch(next, tile - TT);        // in flight during the scan
+        if (tile - TT >= first) fetch(next, tile - TT);        // in flight during the GEMM
         __syncthreads();
-        // backward scan over the tile, maps read into registers first: g_s = P b_s x_s, P = P A_s
-        if (tid < G) {
-            float At[TT][K * K], bt[TT][K];
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
-#pragma unroll
-                for (int q = 0; q < K * K; ++q) At[tt][q] = s_A[tt][q][tid];
-#pragma unroll
-                for (int k = 0; k < K; ++k) bt[tt][k] = s_b[tt][k][tid];
-            }
-#pragma unroll
-            for (int tt = TT - 1; tt >= 0; --tt) {
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    float g = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < K; ++j) g = fmaf(P[k][j], bt[tt][j], g);
-                    const uint16_t hi = to_bf16(g);
-                    s_hi[tid * K + k][tt] = hi;
-                    s_lo[tid * K + k][tt] = to_bf16(g - from_bf16(hi));
-                }
-                float N[K][K];
-#pragma unroll
-                for (int k = 0; k < K; ++k)
-#pragma unroll
-                    for (int j = 0; j < K; ++j) {
-                        float v = 0.0f;
-#pragma unroll
-                        for (int q = 0; q < K; ++q) v = fmaf(P[k][q], At[tt][q * K + j], v);
-                        N[k][j] = v;
-                    }
-#pragma unroll
-                for (int k = 0; k < K; ++k)
-#pragma unroll
-                    for (int j = 0; j < K; ++j) P[k][j] = N[k][j];
-            }
-        }
-        __syncthreads();
-        // carry += (g x)[rows][tokens] . s[tokens][m]
+        // carry += g[rows][tokens] . s[tokens][m]
 #pragma unroll
         for (int q = 0; q < PER_WAVE; ++q) {
-            const int t = wave + 4 * q;
-            if (t < TILES) {
-                const int rt = t % 2, ct = t / 2;
+            const int tl = wave + 4 * q;
+            if (tl < TILES) {
+                const int rt = tl % 2, ct = tl / 2;
                 const int kk = 8 * (lane >> 5);
                 const bf16x8 B = operand(&s_wT[32 * ct + (lane & 31)][kk]);
                 acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(operand(&s_hi[32 * rt + (lane & 31)][kk]), B,
@@ -411,12 +441,12 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
         }
         cur = next;
     }
-    // carry rows (c, k) and Phi = P
+    // carry rows (c, k) and Phi
 #pragma unroll
     for (int q = 0; q < PER_WAVE; ++q) {
-        const int t = wave + 4 * q;
-        if (t < TILES) {
-            const int rt = t % 2, ct = t / 2;
+        const int tl = wave + 4 * q;
+        if (tl < TILES) {
+            const int rt = tl % 2, ct = tl / 2;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int r = 32 * rt + drow(lane, i), m = 32 * ct + (lane & 31);
@@ -428,12 +458,17 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
             }
         }
     }
-    if (tid < G && c0 + tid < a.C) {
-        const long long plane = ((long long)b * a.chunks + chunk_index) * a.C + c0 + tid;
+    if (t == 0) {
 #pragma unroll
-        for (int k = 0; k < K; ++k)
+        for (int e = 0; e < CP; ++e) {
+            if (cr + e < a.C) {
+                const long long plane = ((long long)b * a.chunks + chunk_index) * a.C + cr + e;
 #pragma unroll
-            for (int j = 0; j < K; ++j) a.phi[(plane * K + k) * K + j] = P[k][j];
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int j = 0; j < K; ++j) a.phi[(plane * K + k) * K + j] = Pl[e][k][j];
+            }
+        }
     }
 }
 
