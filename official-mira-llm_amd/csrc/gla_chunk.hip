@@ -14,14 +14,15 @@
 //   waves 0-2  one 32x32 tile each of the masked scores P^T (tiles (s,t) = (0,0), (1,1), (0,1);
 //              the (1,0) tile is all masked) on v_mfma_f32_32x32x16_bf16, then V^T P^T for that
 //              tile with the scores still in registers: an accumulator's 4-row groups are exactly
-//              the B operand of v_mfma_f32_32x32x8_bf16, so P never goes through LDS.
-//   wave 3     the carried-in term S_in Q^T for both token halves, S_in read from a bf16 copy.
+//              the B operand of v_mfma_f32_32x32x8_bf16, so P never goes through LDS. Wave 2 also
+//              computes the carried-in term S_in Q^T e^G of tokens 32-63 into the same tile.
+//   wave 3     the carried-in term of tokens 0-31, S_in read from a bf16 copy.
 //   waves 4-7  the state: wave 4+i keeps S^T rows [32i, 32i+32) (its key block) x 32 value columns
 //              as one float32 accumulator for the whole sequence and writes the bf16 copy of S.
-// Partial output tiles meet in LDS; waves 0 and 1 add them up and store the chunk's outputs as
-// whole 64-byte row pieces while the next chunk is computed. LDS buffers that cross the one
-// barrier per chunk are double buffered by chunk parity (the decay table G, written two chunks
-// ahead, is triple buffered). Global loads run two chunks ahead as raw buffer loads whose
+// Partial output tiles meet in LDS; waves 0 and 1 each add one to their own tile and store the
+// chunk's outputs as whole 64-byte row pieces while the next chunk is computed. LDS buffers
+// that cross the one barrier per chunk are double buffered by chunk parity (the decay table G,
+// written two chunks ahead, is triple buffered). Global loads run two chunks ahead as raw buffer loads whose
 // out-of-range offsets return zeros past the last token; stores past it are dropped the same way.
 //
 // Precision: the state recurrence is float32; the decayed values v e^(G_L - G_s) enter the
@@ -61,7 +62,7 @@ struct alignas(16) Shared {
     uint16_t vh[2][VB][TS];        // (V e^(G_L - G_s))^T, bf16 high part
     uint16_t vl[2][VB][TS];        // its bf16 rounding remainder
     uint16_t s[2][VB][QS];         // bf16 copy of the state entering the chunk, [v][k]
-    float part[2][3][16][64];      // partial output tiles, accumulator order [element][lane]
+    float part[2][2][16][64];      // partial output tiles, accumulator order [element][lane]
     uint16_t out[2][32][OS];       // waves 0, 1: a finished output tile, [token][v]
     float G[3][L];                 // in-chunk cumulative log-decay
 };
@@ -248,11 +249,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         const int buf = chunk & 1;
         f32x16 total = kept;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][wave == 0 ? 1 : 2][i][lane];
-        if (wave == 1) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][0][i][lane];
-        }
+        for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][wave == 0 ? 1 : 0][i][lane];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<u32x2 *>(&sh.out[wave][col][8 * j + 4 * half]) =
@@ -284,6 +281,18 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
             const int t = 32 * tb + col;
             const float Gt = G[t];
             f32x16 out = {};
+            if (wave == 2) {
+                // the carried-in term of tokens 32-63, S_in Q^T e^G, which this tile's V^T P^T adds to
+                f32x16 inter = {};
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+                    inter = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]),
+                        lds_operand8(&sh.q[buf][32 + col][16 * kk + 8 * half]), inter, 0, 0, 0);
+                const float g1 = __builtin_amdgcn_exp2f(Gt * LOG2E);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) out[i] = inter[i] * g1;
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int s0 = 32 * sb + 8 * j + 4 * half;
@@ -306,22 +315,16 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
                 kept = out;
             }
         } else if (wave == 3) {
-            f32x16 acc0 = {}, acc1 = {};
+            // the carried-in term of tokens 0-31
+            f32x16 acc0 = {};
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const bf16x8 st = lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]);
+            for (int kk = 0; kk < 8; ++kk)
                 acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    st, lds_operand8(&sh.q[buf][col][16 * kk + 8 * half]), acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    st, lds_operand8(&sh.q[buf][32 + col][16 * kk + 8 * half]), acc1, 0, 0, 0);
-            }
+                    lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]),
+                    lds_operand8(&sh.q[buf][col][16 * kk + 8 * half]), acc0, 0, 0, 0);
             const float g0 = __builtin_amdgcn_exp2f(G[col] * LOG2E);
-            const float g1 = __builtin_amdgcn_exp2f(G[32 + col] * LOG2E);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sh.part[buf][1][i][lane] = acc0[i] * g0;
-                sh.part[buf][2][i][lane] = acc1[i] * g1;
-            }
+            for (int i = 0; i < 16; ++i) sh.part[buf][1][i][lane] = acc0[i] * g0;
         } else {
             // S^T[32 kb + drow][col] = S[v = col][k = 32 kb + drow]
 #pragma unroll
