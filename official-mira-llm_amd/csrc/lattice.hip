@@ -690,10 +690,13 @@ bool lattice_supported(int K, int M, int dtype) {
 int lattice_lanes(int K, int M) { return lanes_for(K, M); }
 
 int lattice_plan_chunk(int B, int T, int C, int K, int M) {
-    // Enough (b, chunk, channel-group) blocks to put ~8 on every CU, at >= 16 tokens a chunk.
+    // Enough (b, chunk, channel-group) blocks to put ~4 on every CU (as many as are resident at
+    // once), at >= 16 tokens a chunk: longer chunks cost the summary and combine less, and at
+    // B4 T2048 C2048 K2 M64 chunks of 256 tokens beat 128 by 4 % (192 and 320, which leave a
+    // short last chunk, lose 15 %).
     const int G = BLOCK / lanes_for(K, M);
     const long long base = (long long)B * ((C + G - 1) / G);
-    const long long target = 2048;
+    const long long target = 1024;
     if (T <= 32 || base >= target) return T;
     long long chunks = std::min<long long>((target + base - 1) / base, (T + 15) / 16);
     if (chunks <= 1) return T;
