@@ -162,8 +162,8 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
 
     // ---- staging, two chunks ahead: wave w loads tokens [16 (w % 4), +16) of q (w < 4) or k
     // (w >= 4) as 4 row-quads (lane: token 4 r + lane / 16, 16-byte piece lane % 16); waves 4-7
-    // also V tokens [16 (w - 4), +16) (lane: token lane / 4, piece lane % 4); wave 4 the decays of
-    // the chunk after. Two register sets alternate by chunk parity.
+    // also V tokens [16 (w - 4), +16) (lane: token lane / 4, piece lane % 4); wave 3, the lightest,
+    // the decays of the chunk after (and their prefix sum when staging). Two register sets alternate by chunk parity.
     const bool loads_q = wave < 4;
     const int kb = wave - 4;                                          // state waves' key block
     struct Staged { u32x4 rows[4], v; float g; };
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         if (!loads_q)
             in.v = __builtin_amdgcn_raw_buffer_load_b128(
                 vr, token_offset(t0 + (lane >> 2), (lane & 3) * 16), 0, 0);
-        if (wave == 4) in.g = load_decay(chunk + 1);
+        if (wave == 3) in.g = load_decay(chunk + 1);
     };
     float gl = 1.0f;                                                  // state waves: e^(G_L)
     // stage chunk n from registers; G_s, G_L from the decay table (or `local` in the prologue)
@@ -226,10 +226,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
             }
         }
         const float G0 = wave_prefix_sum(load_decay(0));
-        if (kb == 0) {
-            sh.G[0][lane] = G0;
-            sh.G[1][lane] = wave_prefix_sum(set0.g);
-        }
+        if (kb == 0) sh.G[0][lane] = G0;
         const float local[2] = {__shfl(G0, 16 * kb + (lane >> 2), 64),
                                 __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                                               __builtin_bit_cast(int, G0), 63))};
@@ -240,6 +237,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
                 u32x2{pack_bf16(S[4 * j], S[4 * j + 1]), pack_bf16(S[4 * j + 2], S[4 * j + 3])};
     } else {
         stage(0, set0, nullptr);
+        if (wave == 3) sh.G[1][lane] = wave_prefix_sum(set0.g);
     }
     lds_barrier();
 
@@ -272,12 +270,19 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         if (wave < 3) {
             if (wave < 2 && c > 0) finish(c - 1);
             const int sb = wave == 1 ? 1 : 0, tb = wave == 0 ? 0 : 1;
-            f32x16 acc = {};
+            // two accumulation chains (even and odd key steps), added at the end
+            f32x16 acc = {}, acc2 = {};
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
+            for (int kk = 0; kk < 8; kk += 2) {
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                     lds_operand8(&sh.k[buf][32 * sb + col][16 * kk + 8 * half]),
                     lds_operand8(&sh.q[buf][32 * tb + col][16 * kk + 8 * half]), acc, 0, 0, 0);
+                acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    lds_operand8(&sh.k[buf][32 * sb + col][16 * kk + 16 + 8 * half]),
+                    lds_operand8(&sh.q[buf][32 * tb + col][16 * kk + 16 + 8 * half]), acc2, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] += acc2[i];
             const int t = 32 * tb + col;
             const float Gt = G[t];
             f32x16 out = {};
@@ -348,7 +353,7 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
         }
         if (c + 1 < chunks) {
             stage(c + 1, use, nullptr);
-            if (wave == 4) sh.G[(c + 2) % 3][lane] = wave_prefix_sum(use.g);
+            if (wave == 3) sh.G[(c + 2) % 3][lane] = wave_prefix_sum(use.g);
         }
         lds_barrier();
     };
