@@ -575,8 +575,10 @@ void diag_scan_kernel(DiagArgs a, unsigned char *ws, unsigned epoch, int groups_
     }
 }
 
-// one decode token: thread per VEC channels of one sequence
-template <typename IO, int W>
+// one decode token: thread per VEC channels of one sequence. With ALIGNED (ring 8-byte, w and
+// bias 16-byte aligned) a thread's ring history (VEC x H values), conv weights (VEC x W) and bias
+// are read as whole vectors: 8 loads instead of 32 scalar ones.
+template <typename IO, int W, bool ALIGNED>
 __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstate) {
     constexpr int H = W - 1;
     typedef typename Raw<IO>::type RawT;
@@ -595,21 +597,56 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
         const float4 v = *reinterpret_cast<const float4 *>(hstate + at);
         h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
     }
+    // the ring's H past tokens (slot = stream index mod H), conv weights and bias of VEC channels
+    float past[VEC][H], wv[VEC][W], bias[VEC];
+    if constexpr (ALIGNED && sizeof(IO) == 2 && VEC * H == 12 && W == 4) {
+        const unsigned *rw = reinterpret_cast<const unsigned *>(ring + at * H);
+        u32x2 r[3] = {};
+        if (ring) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q) r[q] = reinterpret_cast<const u32x2 *>(rw)[q];
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+#pragma unroll
+            for (int j = 0; j < H; ++j) {
+                const long long stream = a.pos - H + j;
+                const int i = e * H + (int)(((stream % H) + H) % H);   // u16 index within 12
+                const unsigned word = r[i >> 2][(i >> 1) & 1];
+                past[e][j] = (stream >= 0 && ring) ? ((i & 1) ? high_half(word, IO{}) : low_half(word, IO{}))
+                                                   : 0.0f;
+            }
+        const float4 *w4 = reinterpret_cast<const float4 *>(a.w + (long long)d0 * W);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const float4 v = w4[e];
+            wv[e][0] = v.x; wv[e][1] = v.y; wv[e][2] = v.z; wv[e][3] = v.w;
+        }
+        const float4 bv = a.bias ? *reinterpret_cast<const float4 *>(a.bias + d0) : make_float4(0, 0, 0, 0);
+        bias[0] = bv.x; bias[1] = bv.y; bias[2] = bv.z; bias[3] = bv.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const long long d = d0 + e;
+            bias[e] = a.bias ? a.bias[d] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; ++j) wv[e][j] = a.w[d * W + j];
+#pragma unroll
+            for (int j = 0; j < H; ++j) {
+                const long long stream = a.pos - H + j;
+                past[e][j] = (stream >= 0 && ring) ? load(ring + ((long long)b * a.D + d) * H + stream % H) : 0.0f;
+            }
+        }
+    }
     const int write_slot = (int)(a.pos % H);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-        const long long d = d0 + e;
-        float u = a.bias ? a.bias[d] : 0.0f;
+        float u = bias[e];
 #pragma unroll
-        for (int j = 0; j < H; ++j) {
-            const long long stream = a.pos - H + j;
-            const float past = (stream >= 0 && ring) ? load(ring + ((long long)b * a.D + d) * H + stream % H)
-                                                     : 0.0f;
-            u = fmaf(a.w[d * W + j], past, u);
-        }
-        u = fmaf(a.w[d * W + H], xf[e], u);
+        for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], past[e][j], u);
+        u = fmaf(wv[e][H], xf[e], u);
         h[e] = fmaf(af[e], h[e], (1.0f - af[e]) * u);
-        if (ring) ring[((long long)b * a.D + d) * H + write_slot] = x[at + e];
+        if (ring) ring[(at + e) * H + write_slot] = x[at + e];
     }
     *reinterpret_cast<RawT *>(static_cast<IO *>(a.y) + at) = pack<IO>(h);
     *reinterpret_cast<float4 *>(hstate + at) = make_float4(h[0], h[1], h[2], h[3]);
@@ -909,8 +946,13 @@ int scan_typed(const DiagArgs &a, void *ws, size_t bytes, hipStream_t stream) {
 template <typename IO>
 int step_typed(const DiagArgs &a, float *h, hipStream_t stream) {
     const long long threads = (long long)a.B * (a.D / VEC);
-    hipLaunchKernelGGL((diag_step_kernel<IO, 4>), dim3((threads + 255) / 256), dim3(256), 0,
-                       stream, a, h);
+    const auto aligned = [](const void *p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
+    if (aligned(a.ring_out, 8) && aligned(a.w, 16) && aligned(a.bias, 16))
+        hipLaunchKernelGGL((diag_step_kernel<IO, 4, true>), dim3((threads + 255) / 256), dim3(256), 0,
+                           stream, a, h);
+    else
+        hipLaunchKernelGGL((diag_step_kernel<IO, 4, false>), dim3((threads + 255) / 256), dim3(256), 0,
+                           stream, a, h);
     return check_launch("diag_step");
 }
 
