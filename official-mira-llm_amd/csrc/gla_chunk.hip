@@ -9,18 +9,19 @@
 //
 // One workgroup (8 waves) owns one (b, head, block of 32 value columns) and walks the chunks in
 // order; the 4 blocks of a head sit on one XCD, so their shared q and k reads meet in its L2.
-// Each chunk's q and k (token-major) and V^T (raw, and decayed as a bf16 pair) are staged in LDS
-// by all waves from whole-row HBM loads. Roles per chunk:
+// Each chunk's q, k and V (raw, and decayed as a bf16 pair) are staged in LDS token-major, by all
+// waves from whole-row HBM loads with 16-byte LDS writes; operands whose contraction runs over
+// tokens (K^T, V^T) are read with the transposing LDS load of gfx950. Roles per chunk:
 //   waves 0-2  one 32x32 tile each of the masked scores P^T (tiles (s,t) = (0,0), (1,1), (0,1);
 //              the (1,0) tile is all masked) on v_mfma_f32_32x32x16_bf16, then V^T P^T for that
 //              tile with the scores still in registers: an accumulator's 4-row groups are exactly
-//              the B operand of v_mfma_f32_32x32x8_bf16, so P never goes through LDS. Wave 2 also
-//              computes the carried-in term S_in Q^T e^G of tokens 32-63 into the same tile.
-//   wave 3     the carried-in term of tokens 0-31, S_in read from a bf16 copy.
+//              the B operand of v_mfma_f32_32x32x8_bf16, so P never goes through LDS.
+//   wave 3     the carried-in term S_in Q^T e^G of both token halves, S_in read from a bf16 copy.
 //   waves 4-7  the state: wave 4+i keeps S^T rows [32i, 32i+32) (its key block) x 32 value columns
 //              as one float32 accumulator for the whole sequence and writes the bf16 copy of S.
-// Partial output tiles meet in LDS; waves 0 and 1 each add one to their own tile and store the
-// chunk's outputs as whole 64-byte row pieces while the next chunk is computed. LDS buffers
+// Partial output tiles meet in LDS: wave 0 adds the carried-in tile of tokens 0-31 to its own,
+// wave 1 the carried-in tile of tokens 32-63 and wave 2's tile, and both store the chunk's
+// outputs as whole 64-byte row pieces while the next chunk is computed. LDS buffers
 // that cross the one barrier per chunk are double buffered by chunk parity (the decay table G,
 // written two chunks ahead, is triple buffered). Global loads run two chunks ahead as raw buffer loads whose
 // out-of-range offsets return zeros past the last token; stores past it are dropped the same way.
@@ -40,7 +41,7 @@ constexpr int DK = 128, DV = 128;  // head dims
 constexpr int VB = 32;             // value columns per workgroup
 constexpr int BLOCKS = DV / VB;    // workgroups per head
 constexpr int THREADS = 512;       // 8 waves
-constexpr int TS = L + 8;          // LDS row (halfwords) of a token-contiguous tile
+constexpr int VS = VB + 8;         // LDS row (halfwords) of a value tile
 constexpr int QS = DK + 8;         // LDS row (halfwords) of a feature-contiguous tile
 constexpr int OS = VB + 8;         // LDS row (halfwords) of the output staging tile
 constexpr unsigned OUT_OF_RANGE = 0x80000000u;
@@ -58,18 +59,29 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 struct alignas(16) Shared {
     uint16_t q[2][L][QS];          // Q of the chunk, [token][k]
     uint16_t k[2][L][QS];          // K of the chunk, [token][k]
-    uint16_t vt[2][VB][TS];        // V^T of the chunk, [vrow(v)][token]
-    uint16_t vh[2][VB][TS];        // (V e^(G_L - G_s))^T, bf16 high part
-    uint16_t vl[2][VB][TS];        // its bf16 rounding remainder
+    uint16_t vt[2][L][VS];         // V of the chunk, [token][v]
+    uint16_t vh[2][L][VS];         // V e^(G_L - G_s), bf16 high part
+    uint16_t vl[2][L][VS];         // its bf16 rounding remainder
     uint16_t s[2][VB][QS];         // bf16 copy of the state entering the chunk, [v][k]
-    float part[2][2][16][64];      // partial output tiles, accumulator order [element][lane]
+    f32x4 part[2][3][4][64];       // partial output tiles: accumulator elements 4 g..4 g+3 of each lane
     uint16_t out[2][32][OS];       // waves 0, 1: a finished output tile, [token][v]
     float G[3][L];                 // in-chunk cumulative log-decay
 };
 
-// LDS row of value column v in the V^T tiles: rows are permuted (v = 8p + e -> 4e + p) so that
-// the staging writes of one wave (16 tokens x 4 pieces of 8 columns) hit distinct banks
-__device__ __forceinline__ int vrow(int v) { return 4 * (v & 7) + (v >> 3); }
+// Transposed operand reads (ds_read_b64_tr_b16). Within each 16-lane group every lane gives the
+// address of 4 consecutive halfwords, and lane i receives, as element j, halfword i % 4 of the
+// row given by lane 4 j + i / 4 of its group. So when lane p addresses
+//     row r0 + 4 (p / 32) + (p % 16) / 4,  column c0 + 16 ((p / 16) % 2) + 4 (p % 4)
+// of a row-major tile, lane l receives tile[r0 + 4 (l / 32) + j][c0 + l % 32], j = 0..3: the
+// 4 tokens of an MFMA operand whose contraction runs down the tile's rows.
+__device__ __forceinline__ bf16x8 join(s16x4 a, s16x4 b) {
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+__device__ __forceinline__ s16x4 read_down(const uint16_t *tile_row0_col0, int stride, int lane) {
+    const uint16_t *p = tile_row0_col0 + (4 * (lane >> 5) + ((lane & 15) >> 2)) * stride +
+                        16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(p));
+}
 
 // accumulator element i of a 32x32 MFMA tile sits at row drow(lane, i), column lane % 32
 __device__ __forceinline__ int drow(int lane, int i) {
@@ -86,10 +98,6 @@ __device__ __forceinline__ bf16x8 lds_operand8(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
 }
 
-__device__ __forceinline__ s16x4 lds_operand4(const uint16_t *p) {
-    return __builtin_bit_cast(s16x4, *reinterpret_cast<const u32x2 *>(p));
-}
-
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
@@ -99,10 +107,6 @@ __device__ __forceinline__ uint16_t to_bf16(float v) {
 }
 
 __device__ __forceinline__ float from_bf16(uint32_t h) { return __uint_as_float(h << 16); }
-
-__device__ __forceinline__ uint16_t half_of(const u32x4 &w, int i) {
-    return static_cast<uint16_t>(w[i >> 1] >> ((i & 1) * 16));
-}
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp(float x) {
@@ -200,15 +204,17 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
             const float Gs = local ? local[0] : sh.G[n % 3][s];
             gl = __builtin_amdgcn_exp2f(GL * LOG2E);
             const float scale = __builtin_amdgcn_exp2f((GL - Gs) * LOG2E);
+            u32x4 hi, lo;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t raw = half_of(in.v, e);
-                const float w = from_bf16(raw) * scale;
-                const uint16_t hi = to_bf16(w);
-                sh.vt[buf][vrow(v0 + e)][s] = raw;
-                sh.vh[buf][vrow(v0 + e)][s] = hi;
-                sh.vl[buf][vrow(v0 + e)][s] = to_bf16(w - from_bf16(hi));
+            for (int j = 0; j < 4; ++j) {
+                const float w0 = from_bf16(in.v[j] & 0xffffu) * scale;
+                const float w1 = __uint_as_float(in.v[j] & 0xffff0000u) * scale;
+                hi[j] = pack_bf16(w0, w1);
+                lo[j] = pack_bf16(w0 - from_bf16(hi[j] & 0xffffu), w1 - __uint_as_float(hi[j] & 0xffff0000u));
             }
+            *reinterpret_cast<u32x4 *>(&sh.vt[buf][s][v0]) = in.v;
+            *reinterpret_cast<u32x4 *>(&sh.vh[buf][s][v0]) = hi;
+            *reinterpret_cast<u32x4 *>(&sh.vl[buf][s][v0]) = lo;
         }
     };
 
@@ -241,13 +247,24 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
     }
     lds_barrier();
 
+    auto put_part = [&](f32x4 (&dst)[4][64], const f32x16 &v) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) dst[g][lane] = f32x4{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    };
+    auto add_part = [&](f32x16 &v, const f32x4 (&src)[4][64]) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 x = src[g][lane];
+            v[4 * g] += x[0]; v[4 * g + 1] += x[1]; v[4 * g + 2] += x[2]; v[4 * g + 3] += x[3];
+        }
+    };
     f32x16 kept = {};                                                 // waves 0, 1: last tile
     // waves 0, 1: add the partial tiles of chunk `chunk`, store its 32 tokens x 32 values
     auto finish = [&](int chunk) {
         const int buf = chunk & 1;
         f32x16 total = kept;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) total[i] += sh.part[buf][wave == 0 ? 1 : 0][i][lane];
+        add_part(total, sh.part[buf][wave == 0 ? 1 : 2]);
+        if (wave == 1) add_part(total, sh.part[buf][0]);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             *reinterpret_cast<u32x2 *>(&sh.out[wave][col][8 * j + 4 * half]) =
@@ -286,18 +303,6 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
             const int t = 32 * tb + col;
             const float Gt = G[t];
             f32x16 out = {};
-            if (wave == 2) {
-                // the carried-in term of tokens 32-63, S_in Q^T e^G, which this tile's V^T P^T adds to
-                f32x16 inter = {};
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-                    inter = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]),
-                        lds_operand8(&sh.q[buf][32 + col][16 * kk + 8 * half]), inter, 0, 0, 0);
-                const float g1 = __builtin_amdgcn_exp2f(Gt * LOG2E);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) out[i] = inter[i] * g1;
-            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int s0 = 32 * sb + 8 * j + 4 * half;
@@ -310,41 +315,47 @@ __global__ __launch_bounds__(THREADS) void gla_chunk_kernel(GlaArgs a) {
                 }
                 const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16(p[0], p[1]),
                                                                  pack_bf16(p[2], p[3])});
-                out = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(lds_operand4(&sh.vt[buf][vrow(col)][s0]),
-                                                               pb, out, 0, 0, 0);
+                out = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(
+                    read_down(&sh.vt[buf][32 * sb + 8 * j][0], VS, lane), pb, out, 0, 0, 0);
             }
             if (wave == 2) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sh.part[buf][0][i][lane] = out[i];
+                put_part(sh.part[buf][0], out);
             } else {
                 kept = out;
             }
         } else if (wave == 3) {
-            // the carried-in term of tokens 0-31
-            f32x16 acc0 = {};
+            // the carried-in term S_in Q^T e^G of both token halves, sharing the S_in operand
+            f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
+            for (int kk = 0; kk < 8; ++kk) {
+                const bf16x8 sop = lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]);
                 acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    lds_operand8(&sh.s[buf][col][16 * kk + 8 * half]),
-                    lds_operand8(&sh.q[buf][col][16 * kk + 8 * half]), acc0, 0, 0, 0);
+                    sop, lds_operand8(&sh.q[buf][col][16 * kk + 8 * half]), acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    sop, lds_operand8(&sh.q[buf][32 + col][16 * kk + 8 * half]), acc1, 0, 0, 0);
+            }
             const float g0 = __builtin_amdgcn_exp2f(G[col] * LOG2E);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sh.part[buf][1][i][lane] = acc0[i] * g0;
+            const float g1 = __builtin_amdgcn_exp2f(G[32 + col] * LOG2E);
+            put_part(sh.part[buf][1], acc0 * g0);
+            put_part(sh.part[buf][2], acc1 * g1);
         } else {
             // S^T[32 kb + drow][col] = S[v = col][k = 32 kb + drow]
 #pragma unroll
             for (int i = 0; i < 16; ++i) S[i] *= gl;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const int s0 = 16 * kk + 8 * half;
-                bf16x8 kop;
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    kop[i] = __builtin_bit_cast(__bf16, sh.k[buf][s0 + i][32 * kb + col]);
-                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vh[buf][vrow(col)][s0]),
-                                                            S, 0, 0, 0);
-                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, lds_operand8(&sh.vl[buf][vrow(col)][s0]),
-                                                            S, 0, 0, 0);
+                // the 16 tokens of step kk as two transposed reads: element i of lane half h is
+                // token 16 kk + 4 h + i (i < 4) or 16 kk + 8 + 4 h + (i - 4), the same
+                // permutation of the contraction in both operands
+                const int r0 = 16 * kk;
+                const bf16x8 kop = join(read_down(&sh.k[buf][r0][32 * kb], QS, lane),
+                                        read_down(&sh.k[buf][r0 + 8][32 * kb], QS, lane));
+                const bf16x8 vho = join(read_down(&sh.vh[buf][r0][0], VS, lane),
+                                        read_down(&sh.vh[buf][r0 + 8][0], VS, lane));
+                const bf16x8 vlo = join(read_down(&sh.vl[buf][r0][0], VS, lane),
+                                        read_down(&sh.vl[buf][r0 + 8][0], VS, lane));
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, vho, S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, vlo, S, 0, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
