@@ -1,6 +1,6 @@
 """Benchmark of the Mira mixer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-stack]
 
 Headline (BASELINE.json `metric`, `configs[1]`): bf16 prefill of the depthwise causal conv
 (width 4) + diagonal decay scan at B=8, T=4096, D=2048 with a carried-in fp32 state, inputs
@@ -9,8 +9,9 @@ tokens/s over exactly K timed steps. Beside it: the decode leg (`configs[3]`, ba
 128 steps of conv+diag and GLA matrix-state updates), the roofline of the dominant kernel from
 HIP events on the launch stream, and the CPU oracle timed on the host's cores on a bounded
 sample of the same workload. Also reported, not headline: the GLA chunked prefill (`configs[2]`,
-% HBM and % MFMA) and the reference operator matrix_lattice_iir at the cfg5 mixer geometry
-(K=2, M=64). Prints one JSON line.
+% HBM and % MFMA), the reference operator matrix_lattice_iir at the cfg5 mixer geometry
+(K=2, M=64), and the 24-layer MiraLLM forward of `configs[4]` with the mixer's and the scan's
+share of its time (skip it with --no-stack). Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -35,6 +36,8 @@ def parse():
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--no-stack", action="store_true",
+                        help="skip the 24-layer MiraLLM forward (BASELINE configs[4])")
     parser.add_argument("--decode-steps", type=int, default=128)
     parser.add_argument("--calibrate", action="store_true",
                         help="also run an elementwise kernel of known traffic (reads and writes "
@@ -208,6 +211,87 @@ def lattice_leg(torch, mira, steps, warmup):
             "shape": f"B={B} T={T} C={C} K={K} M={M}"}
 
 
+def stack_leg(torch, steps, warmup):
+    """24 random-init MiraBlocks (d_model 2048, lattice_d_e 2048, K=2,
+    d_m 64, d_r 128, FFN 8192 SiLU-MLP), vocab 32000 with the tied head, weights N(0, 0.02^2),
+    bf16, forward prefill of B=4 T=2048 uniform token ids with no cache. A step is one whole
+    forward including the logits. One further forward carries HIP events around every mixer and
+    every scan launch (matrix_lattice_iir) for the time shares."""
+    from mira_amd import mixer as mixer_module
+    from mira_amd.llm import MiraLLM
+
+    B, T, V, L, d, C, M, R, H = 4, 2048, 32000, 24, 2048, 2048, 64, 128, 8192
+    with torch.device("cuda"):
+        torch.manual_seed(5)
+        model = MiraLLM(vocab_size=V, n_layer=L, n_embd=d, lattice_d_e=C, lattice_order=2,
+                        memory_dimension=M, coefficient_bottleneck=R, ffn_hidden=H)
+    model = model.to(torch.bfloat16).eval()
+    g = torch.Generator(device="cuda").manual_seed(6)
+    ids = torch.randint(0, V, (B, T), device="cuda", generator=g)
+    stream = torch.cuda.current_stream()
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(ids)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            model(ids)
+        end.record(stream)
+        torch.cuda.synchronize()
+        forward_s = start.elapsed_time(end) * 1e-3 / steps
+
+        spans = {"mixer": [], "scan": []}
+
+        def opener(kind):
+            def hook(*_):
+                event = torch.cuda.Event(enable_timing=True)
+                event.record(stream)
+                spans[kind].append([event])
+            return hook
+
+        def closer(kind):
+            def hook(*_):
+                event = torch.cuda.Event(enable_timing=True)
+                event.record(stream)
+                spans[kind][-1].append(event)
+            return hook
+
+        scan = mixer_module.plugin.matrix_lattice_iir
+
+        def timed_scan(*args, **kwargs):
+            opener("scan")()
+            result = scan(*args, **kwargs)
+            closer("scan")()
+            return result
+
+        handles = []
+        for block in model.blocks:
+            handles.append(block.mixer.register_forward_pre_hook(opener("mixer")))
+            handles.append(block.mixer.register_forward_hook(closer("mixer")))
+        mixer_module.plugin.matrix_lattice_iir = timed_scan
+        try:
+            start.record(stream)
+            model(ids)
+            end.record(stream)
+            torch.cuda.synchronize()
+        finally:
+            mixer_module.plugin.matrix_lattice_iir = scan
+            for handle in handles:
+                handle.remove()
+        whole = start.elapsed_time(end)
+        share = {k: sum(a.elapsed_time(b) for a, b in v) / whole for k, v in spans.items()}
+    gemm_per_token = 2 * L * (d * (C + M) + d * C + d * R + R * (7 * C + 3 * M) + C * d + 2 * d * H)
+    gemm_per_token += 2 * d * V
+    scan_per_token = L * C * M * (9 * 2 + 4)
+    del model
+    torch.cuda.empty_cache()
+    return {"tokens": B * T, "forward_s": forward_s, "mixer_share": share["mixer"],
+            "scan_share": share["scan"], "flops": (gemm_per_token + scan_per_token) * B * T,
+            "shape": f"{L} layers, d_model {d}, d_e {C}, K 2, d_m {M}, d_r {R}, FFN {H}, "
+                     f"vocab {V}; B={B} T={T}"}
+
+
 def cpu_leg(budget_s=12.0):
     """The oracle's restatement of the reference CPU mixer (the batched per-token formulation of
     model/mira_mixer.py:319-387, numpy float32) on the cfg2 workload realised as the K=1 lattice,
@@ -262,6 +346,7 @@ def main():
     gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3)
     gla_hbm = gla["algorithmic"] / gla["kernel_s"] / 1e9
     lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2)
+    stack = None if args.no_stack else stack_leg(torch, 3, 1)
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
     traffic = traffic_from_profiles("diag_column_kernel")
     gla_achieved = decode["gla_bytes"] / decode["gla_kernel_s"] / 1e9
@@ -325,6 +410,16 @@ def main():
                      "flops": lat["flops"]}},
         "watchdog": prefill["watchdog"],
     }
+    if stack is not None:
+        line["stack"] = {
+            "metric": "cfg5 forward prefill tokens/s (24 MiraBlocks, bf16, no cache)",
+            "shape": stack["shape"], "unit": "tokens/s",
+            "value": stack["tokens"] / stack["forward_s"],
+            "ms_per_forward": round(stack["forward_s"] * 1e3, 2),
+            "mixer_share": round(stack["mixer_share"], 4),
+            "scan_share": round(stack["scan_share"], 4),
+            "tflops": round(stack["flops"] / stack["forward_s"] / 1e12, 1),
+            "flops_per_forward": stack["flops"]}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_leg()
     if args.calibrate:

@@ -5,5 +5,7 @@
   mira_amd.hardware      device selection (kernel/hardware.py's API), HIP only
   mira_amd.prefix_cache  the decode-state cache (model/prefix_cache.py's API)
   mira_amd.mixer         MiraMixer with the reference constructor and forward signature
+  mira_amd.block         RMSNorm, FeedForward and MiraBlock (model/mira_block.py's API)
+  mira_amd.llm           MiraLLM, the stack of blocks between the tied embedding and head
 """
 from . import mira  # noqa: F401

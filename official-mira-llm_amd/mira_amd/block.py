@@ -1,0 +1,87 @@
+"""MiraBlock on the MI355X plugin: one MIRA layer, RMSNorm -> MiraMixer on the residual stream,
+RMSNorm -> feed-forward on the residual stream (model/mira_block.py:156-205).
+
+The constructor and forward keep the reference's signatures, so a MiraLLM assembled from these
+blocks is called as the reference's is. The mixer is mira_amd.mixer.MiraMixer, whose scan runs on
+the HIP library; the norms and the feed-forward are PyTorch (their GEMMs go to hipBLASLt).
+Mixture-of-experts feed-forwards (model/mira_block.py:51-145) are not part of the scan's hot path
+and are not built: a `moe` argument raises.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .mixer import MiraMixer
+
+
+class RMSNorm(nn.Module):
+    """x / sqrt(mean(x^2) + eps) * weight (+ bias), computed in float32 and returned in the
+    input's dtype (model/mira_block.py:21-35)."""
+
+    def __init__(self, width: int, eps: float = 1e-8, bias: bool = False):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(int(width)))
+        self.bias = nn.Parameter(torch.zeros(int(width))) if bias else None
+        self.eps = float(eps)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        z = x.float()
+        z = z * torch.rsqrt(z.square().mean(dim=-1, keepdim=True) + self.eps) * self.weight.float()
+        if self.bias is not None:
+            z = z + self.bias.float()
+        return z.to(x.dtype)
+
+
+class FeedForward(nn.Module):
+    """down(SiLU(up(x))) with biases; hidden width 4 x width unless given
+    (model/mira_block.py:38-48). Not SwiGLU."""
+
+    def __init__(self, width: int, dropout: float = 0.0, hidden: int = None):
+        super().__init__()
+        hidden = int(hidden) if hidden else 4 * int(width)
+        self.up = nn.Linear(width, hidden)
+        self.down = nn.Linear(hidden, width)
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, x):
+        return self.dropout(self.down(F.silu(self.up(x))))
+
+
+class MiraBlock(nn.Module):
+    def __init__(self, width: int, dropout: float = 0.0, lattice_order: int = 2, d_e: int = None,
+                 coefficient_bottleneck: int = None, memory_dimension: int = 16,
+                 ffn_hidden: int = None, positive_poles: bool = False,
+                 lattice_initializer: str = "W_uniform_b_jeffreys", lattice_init_horizon=None,
+                 arch: str = "cauchy_x_hyperbolic", moe: dict = None):
+        super().__init__()
+        if moe:
+            raise ValueError("mixture-of-experts feed-forwards are not built on the MI355X path")
+        width = int(width)
+        d_e = 2 * width if d_e is None else int(d_e)
+        coefficient_bottleneck = (max(1, width // 16) if coefficient_bottleneck is None
+                                  else int(coefficient_bottleneck))
+        self.rn1 = RMSNorm(width)
+        self.mixer = MiraMixer(width, lattice_order, d_e, coefficient_bottleneck, memory_dimension,
+                               dropout=dropout, positive_poles=positive_poles,
+                               lattice_initializer=lattice_initializer,
+                               lattice_init_horizon=lattice_init_horizon, arch=arch)
+        self.rn2 = RMSNorm(width)
+        self.ffn = FeedForward(width, dropout, hidden=ffn_hidden)
+
+    def post_init(self, n_layer: int):
+        """The residual-output projections drawn with std 0.02 / sqrt(2 n_layer)
+        (model/mira_block.py:193-201). The reference also places the lattice poles here
+        (model/mira_initializer.py); that initializer is not built, so the coefficient
+        projection keeps the model-wide initialisation."""
+        std = 0.02 / math.sqrt(2 * int(n_layer))
+        nn.init.normal_(self.mixer.out_proj.weight, mean=0.0, std=std)
+        nn.init.normal_(self.ffn.down.weight, mean=0.0, std=std)
+        return self
+
+    def forward(self, x, attn_mask=None, cache=None, layer=None):
+        x = x + self.mixer(self.rn1(x), attn_mask, cache, layer)
+        return x + self.ffn(self.rn2(x))

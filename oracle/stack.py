@@ -1,0 +1,107 @@
+"""CPU restatement of the MIRA layer stack around the scan -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module.
+
+Restates, in numpy (float64 by default), what surrounds the lattice scan in a MIRA model:
+  * RMSNorm                                  model/mira_block.py:21-35
+  * FeedForward, down(SiLU(up(x)))           model/mira_block.py:38-48
+  * MiraMixer.forward: the packed input / gate / control projection, SiLU of the control, the
+    coefficient projection split alpha | beta | rho | nu, s = SiLU(raw write), the scan
+    (oracle.lattice.lattice_scan_sequential), out_proj and the re-mask
+                                             model/mira_mixer.py:657-712, 714-856
+  * MiraBlock.forward                        model/mira_block.py:203-205
+  * MiraLLM trunk and tied head              model/mira_llm.py:234-299, 345-351
+
+Parameters come as a dict of numpy arrays keyed by the state_dict names of mira_amd.llm.MiraLLM
+(`blocks.<i>.mixer.input_projection.weight`, ...). An optional `rnd` function is applied where a
+half-precision PyTorch model stores a tensor (every norm, projection, SiLU, scan and residual
+output), so a bf16 model is compared with the same arithmetic rounded at the same places; without
+it everything stays in the working precision.
+
+Pinning (tests/test_stack.py): RMSNorm rows have unit root-mean-square (times the weight) and a
+constant row maps to +-1; a mixer whose coefficient projection is zero outputs exactly zero (rho
+routes the readout); a mixer whose coefficients are constants set through the projection bias
+reduces, at K=1 and d_m=1, to the closed-form first-order recurrence (a wrong span order or a
+transposed split fails it); a masked token leaves every later output unchanged whatever its id;
+and a prompt followed by single-token steps through the carried state equals the one-shot
+forward.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import lattice as L
+
+
+def silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def _r(rnd, a):
+    return a if rnd is None else rnd(a)
+
+
+def linear(x, weight, bias=None):
+    y = x @ weight.T
+    return y if bias is None else y + bias
+
+
+def rmsnorm(x, weight, bias=None, eps=1e-8, rnd=None):
+    """x / sqrt(mean(x^2) + eps) * weight (+ bias), model/mira_block.py:28-35."""
+    z = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * weight
+    return _r(rnd, z if bias is None else z + bias)
+
+
+def feed_forward(x, p, prefix, rnd=None):
+    """down(SiLU(up(x))), model/mira_block.py:47-48."""
+    hidden = _r(rnd, silu(_r(rnd, linear(x, p[prefix + "up.weight"], p[prefix + "up.bias"]))))
+    return _r(rnd, linear(hidden, p[prefix + "down.weight"], p[prefix + "down.bias"]))
+
+
+def mixer_forward(x, p, prefix, order, channels, memory, arch, valid=None, state=None,
+                  dtype=np.float64, rnd=None):
+    """MiraMixer.forward on normalised input x [B,T,d]; returns (out [B,T,d], final state)."""
+    B, T, _ = x.shape
+    signal_write = _r(rnd, linear(x, p[prefix + "input_projection.weight"]))
+    gamma = _r(rnd, linear(x, p[prefix + "to_gate.weight"], p[prefix + "to_gate.bias"]))
+    control = _r(rnd, silu(_r(rnd, linear(x, p[prefix + "to_control.weight"],
+                                          p[prefix + "to_control.bias"]))))
+    coefficients = _r(rnd, linear(control, p[prefix + "coefficient_projection.weight"],
+                                  p[prefix + "coefficient_projection.bias"]))
+    signal, raw_write = signal_write[..., :channels], signal_write[..., channels:]
+    a, r = channels * order, channels * (order + 1)
+    alpha = coefficients[..., :a].reshape(B, T, channels, order)
+    beta = coefficients[..., a:2 * a].reshape(B, T, channels, order)
+    rho = coefficients[..., 2 * a:2 * a + r].reshape(B, T, channels, order + 1)
+    read = coefficients[..., 2 * a + r:].reshape(B, T, order + 1, memory)
+    y, final = L.lattice_scan_sequential(signal, alpha, rho, gamma, _r(rnd, silu(raw_write)),
+                                         read, beta, valid=valid, state=state, arch=arch,
+                                         dtype=dtype)
+    out = _r(rnd, linear(_r(rnd, y), p[prefix + "out_proj.weight"]))
+    if valid is not None:
+        out = np.where(np.asarray(valid, bool)[..., None], out, 0.0)
+    return out, final
+
+
+def block_forward(x, p, prefix, cfg, valid=None, state=None, rnd=None):
+    """x + mixer(rn1(x)), then + ffn(rn2(x)), model/mira_block.py:203-205."""
+    mixed, final = mixer_forward(rmsnorm(x, p[prefix + "rn1.weight"], rnd=rnd), p,
+                                 prefix + "mixer.", cfg["lattice_order"], cfg["lattice_d_e"],
+                                 cfg["memory_dimension"], cfg["arch"], valid=valid, state=state,
+                                 rnd=rnd)
+    x = _r(rnd, x + mixed)
+    ffn = feed_forward(rmsnorm(x, p[prefix + "rn2.weight"], rnd=rnd), p, prefix + "ffn.", rnd=rnd)
+    return _r(rnd, x + ffn), final
+
+
+def llm_forward(ids, p, cfg, valid=None, states=None, rnd=None):
+    """Logits [B,T,vocab] of MiraLLM over token ids [B,T]; `states` (one per layer, or None)
+    are the carried lattice states, returned updated."""
+    x = p["tok.weight"][ids]
+    finals = []
+    for i in range(cfg["n_layer"]):
+        x, final = block_forward(x, p, f"blocks.{i}.", cfg, valid=valid,
+                                 state=None if states is None else states[i], rnd=rnd)
+        finals.append(final)
+    h = rmsnorm(x, p["lnf.weight"], p["lnf.bias"], rnd=rnd)
+    return _r(rnd, h @ p["head.weight"].T), finals
