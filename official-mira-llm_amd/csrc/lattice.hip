@@ -15,7 +15,9 @@
 //            enters every chunk over its carry slot.
 //   replay   per (b, chunk, c): the chunk from its entering state with the readout and the gate;
 //            the last chunk stores the final state. With one chunk this is the whole scan, and at
-//            T = 1 it is the decode step.
+//            T = 1 it is the decode step. Stage K's level is never kept, so the replay reads it
+//            out as rc_K sum_m V^(K-1) nu_K + rs_K x sum_m s nu_K instead of forming it per m:
+//            5K - 1 operations per (t, c, m) instead of 5K + 2.
 // A block is 256 threads = G channels x L lanes; lane l of a channel owns M/L memory slots, so a
 // channel's K x M state lives in registers. Per tile of TT tokens the block stages in LDS the
 // write and read vectors s, nu (per (b, t), shared by every channel) and, per (token, channel),
@@ -580,27 +582,34 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
 #pragma unroll
                     for (int k = 0; k <= K; ++k) rho[k] = cf[(2 * K + 1 + k) * G];
                     const float gate = cf[(3 * K + 2) * G];
+                    const float rcx = rc[K - 1] * xv;
                     const float *nu = s_read + tt * (K + 1) * M;
-                    float acc[K + 1];
+                    float acc[K + 1], sig = 0.0f;
 #pragma unroll
                     for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
 #pragma unroll
                     for (int v = 0; v < MV; ++v) {
                         const int m = slot<M, L>(lane, v);
-                        float U = xv * s_write[tt * M + m];
+                        const float sv = s_write[tt * M + m];
+                        // stage K's level rc_K V^(K-1) + rs_K x s is only read out: its sum over m
+                        // is rc_K sum V^(K-1) nu_K + rs_K x sum s nu_K, so only U' is formed here
+                        sig = fmaf(sv, nu[K * M + m], sig);
+                        acc[K] = fmaf(V[K - 1][v], nu[K * M + m], acc[K]);
+                        float U = fmaf(rcx, sv, -(rs[K - 1] * V[K - 1][v]));
 #pragma unroll
-                        for (int k = K; k >= 1; --k) {
+                        for (int k = K - 1; k >= 1; --k) {
                             const float delayed = V[k - 1][v];
-                            const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
-                            U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
-                            acc[k] = fmaf(level, nu[k * M + m], acc[k]);
-                            if (k < K) V[k][v] = level;
+                            const float up = rs[k - 1] * U, down = rs[k - 1] * delayed;
+                            V[k][v] = fmaf(rc[k - 1], delayed, up);        // level_k, kept
+                            U = fmaf(rc[k - 1], U, -down);
+                            acc[k] = fmaf(V[k][v], nu[k * M + m], acc[k]);
                         }
                         V[0][v] = U;
                         acc[0] = fmaf(U, nu[m], acc[0]);
                     }
+                    y = rho[K] * fmaf(rc[K - 1], acc[K], rs[K - 1] * xv * sig);
 #pragma unroll
-                    for (int k = 0; k <= K; ++k) y = fmaf(rho[k], acc[k], y);
+                    for (int k = 0; k < K; ++k) y = fmaf(rho[k], acc[k], y);
                     y = gate * lane_sum<L>(y);
                 }
                 if (lane == 0) s_out[tt * G + cl] = y;
