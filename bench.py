@@ -207,8 +207,32 @@ def lattice_leg(torch, mira, steps, warmup):
     call_s = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) * 1e-3 / steps
     nbytes = B * T * C * 2 * (3 * K + 4) + B * T * 2 * M * (K + 2) + 2 * B * K * C * M * 4
     flops = B * T * C * M * (9 * K + 4)
+
+    # the operator's decode: one token for 256 sequences with the state updated in place
+    # (matrix_lattice_step, the prefix-cache step of a served MIRA layer)
+    SB = 256
+    step_in = [(torch.randn(SB, 1, *shape, device="cuda", generator=g) * 0.12).to(bf)
+               for shape in ((C,), (C, K), (C, K + 1), (C,), (M,), (K + 1, M), (C, K))]
+    step_in[4] = torch.nn.functional.silu(step_in[4])
+    step_state = torch.randn(SB, K, C, M, device="cuda", generator=g) * 0.1
+    step_out = torch.empty(SB, 1, C, device="cuda", dtype=bf)
+
+    def step():
+        mira.matrix_lattice_step(*step_in, step_state, out=step_out, inplace=True)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    starts[0].record(stream)
+    for _ in range(steps * 4):
+        step()
+    ends[0].record(stream)
+    torch.cuda.synchronize()
+    step_s = starts[0].elapsed_time(ends[0]) * 1e-3 / (steps * 4)
+    step_bytes = 2 * SB * K * C * M * 4 + SB * C * 2 * (3 * K + 4) + SB * 2 * M * (K + 2)
     return {"tokens": B * T, "call_s": call_s, "bytes": nbytes, "flops": flops,
-            "shape": f"B={B} T={T} C={C} K={K} M={M}"}
+            "shape": f"B={B} T={T} C={C} K={K} M={M}", "step_s": step_s,
+            "step_bytes": step_bytes, "step_shape": f"B={SB} T=1 C={C} K={K} M={M}"}
 
 
 def stack_leg(torch, steps, warmup):
@@ -407,7 +431,15 @@ def main():
             "valu": {"achieved": round(lat["flops"] / lat["call_s"] / 1e12, 1),
                      "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(lat["flops"] / lat["call_s"] / 1e12 / 157.3, 4),
-                     "flops": lat["flops"]}},
+                     "flops": lat["flops"]},
+            "decode_step": {
+                "shape": lat["step_shape"], "unit": "steps/s", "value": 1.0 / lat["step_s"],
+                "step_us": round(lat["step_s"] * 1e6, 1),
+                "roofline": {"bound": "hbm", "kernel": "lattice_step_kernel",
+                             "achieved": round(lat["step_bytes"] / lat["step_s"] / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(lat["step_bytes"] / lat["step_s"] / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": lat["step_bytes"]}}},
         "watchdog": prefill["watchdog"],
     }
     if stack is not None:

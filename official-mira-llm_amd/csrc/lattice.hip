@@ -630,11 +630,134 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// decode step (T = 1): a stream of the state
+// ---------------------------------------------------------------------------------------------
+// One token moves the whole [B,K,C,M] float32 state through HBM once each way, so the step is a
+// stream: a block takes one sequence b and 256 / (M/8) channels, a lane owns 8 consecutive memory
+// slots of one channel (two 16-byte accesses per state row), s and nu of the sequence are staged
+// in LDS once, and the stage maps run once per channel. The update and readout are the replay's
+// (stage K's level read out through sum V^(K-1) nu_K and sum s nu_K). A masked token copies the
+// state and writes 0.
+__host__ __device__ constexpr bool step_kernel_serves(int K, int M) { return K <= 4 && M >= 8 && M <= 128; }
+
+template <typename IO, int K, int M>
+__global__ __launch_bounds__(BLOCK) void lattice_step_kernel(LatticeArgs a) {
+    constexpr int LPC = M / 8;                   // lanes of a channel
+    constexpr int CPB = BLOCK / LPC;             // channels of a block
+    constexpr int NC = coef_count(K, true);
+    const int groups = (a.C + CPB - 1) / CPB;
+    const int b = blockIdx.x / groups, c0 = (blockIdx.x % groups) * CPB;
+    const int tid = threadIdx.x, cl = tid / LPC, part = tid % LPC, c = c0 + cl;
+    __shared__ __align__(16) float s_sn[(K + 2) * M];     // s, then nu_0 .. nu_K
+    __shared__ float s_coef[NC * CPB];                     // [quantity][channel]
+    const IO *write = static_cast<const IO *>(a.write);
+    const IO *read = static_cast<const IO *>(a.read);
+    for (int i = tid; i < (K + 2) * M; i += BLOCK)
+        s_sn[i] = i < M ? load(write + (long long)b * M + i)
+                        : load(read + (long long)b * a.read_row + (i - M));
+    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    for (int i = tid; i < CPB && c0 + i < a.C; i += BLOCK) {
+        const int ch = c0 + i;
+        const IO *alpha = static_cast<const IO *>(a.alpha) + (long long)b * a.alpha_row + (long long)ch * K;
+        const IO *beta = static_cast<const IO *>(a.beta) + (long long)b * a.beta_row + (long long)ch * K;
+        const IO *rho = static_cast<const IO *>(a.rho) + (long long)b * a.rho_row + (long long)ch * (K + 1);
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float rc, rs;
+            stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc, rs);
+            s_coef[k * CPB + i] = rc;
+            s_coef[(K + k) * CPB + i] = rs;
+        }
+        s_coef[2 * K * CPB + i] = load(static_cast<const IO *>(a.x) + (long long)b * a.x_row + ch);
+#pragma unroll
+        for (int k = 0; k <= K; ++k) s_coef[(2 * K + 1 + k) * CPB + i] = load(rho + k);
+        s_coef[(3 * K + 2) * CPB + i] =
+            silu(load(static_cast<const IO *>(a.gamma) + (long long)b * a.gamma_row + ch));
+    }
+    __syncthreads();
+    if (c >= a.C) return;                        // whole channel groups; no barrier follows
+    const bool valid = a.valid ? a.valid[b] != 0 : true;
+    float V[K][8];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        if (a.state_in) {
+            const float4 *src = reinterpret_cast<const float4 *>(
+                a.state_in + (((long long)b * K + k) * a.C + c) * M + part * 8);
+            const float4 lo = src[0], hi = src[1];
+            V[k][0] = lo.x; V[k][1] = lo.y; V[k][2] = lo.z; V[k][3] = lo.w;
+            V[k][4] = hi.x; V[k][5] = hi.y; V[k][6] = hi.z; V[k][7] = hi.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) V[k][e] = 0.0f;
+        }
+    }
+    float y = 0.0f;
+    if (valid) {
+        float rc[K], rs[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) { rc[k] = s_coef[k * CPB + cl]; rs[k] = s_coef[(K + k) * CPB + cl]; }
+        const float xv = s_coef[2 * K * CPB + cl];
+        const float rcx = rc[K - 1] * xv;
+        float sv[8], nv[K + 1][8];
+#pragma unroll
+        for (int q = 0; q <= K + 1; ++q) {
+            const float4 *src = reinterpret_cast<const float4 *>(s_sn + q * M + part * 8);
+            const float4 lo = src[0], hi = src[1];
+            float *dst = q == 0 ? sv : nv[q - 1];
+            dst[0] = lo.x; dst[1] = lo.y; dst[2] = lo.z; dst[3] = lo.w;
+            dst[4] = hi.x; dst[5] = hi.y; dst[6] = hi.z; dst[7] = hi.w;
+        }
+        float acc[K + 1], sig = 0.0f;
+#pragma unroll
+        for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            sig = fmaf(sv[e], nv[K][e], sig);
+            acc[K] = fmaf(V[K - 1][e], nv[K][e], acc[K]);
+            float U = fmaf(rcx, sv[e], -(rs[K - 1] * V[K - 1][e]));
+#pragma unroll
+            for (int k = K - 1; k >= 1; --k) {
+                const float delayed = V[k - 1][e];
+                const float up = rs[k - 1] * U, down = rs[k - 1] * delayed;
+                V[k][e] = fmaf(rc[k - 1], delayed, up);
+                U = fmaf(rc[k - 1], U, -down);
+                acc[k] = fmaf(V[k][e], nv[k][e], acc[k]);
+            }
+            V[0][e] = U;
+            acc[0] = fmaf(U, nv[0][e], acc[0]);
+        }
+        y = s_coef[(3 * K + 1) * CPB + cl] * fmaf(rc[K - 1], acc[K], rs[K - 1] * xv * sig);
+#pragma unroll
+        for (int k = 0; k < K; ++k) y = fmaf(s_coef[(2 * K + 1 + k) * CPB + cl], acc[k], y);
+        y = s_coef[(3 * K + 2) * CPB + cl] * lane_sum<LPC>(y);
+    }
+    if (part == 0) static_cast<IO *>(a.out)[(long long)b * a.C + c] = from_float<IO>(y);
+    if (a.state_out) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float4 *dst = reinterpret_cast<float4 *>(
+                a.state_out + (((long long)b * K + k) * a.C + c) * M + part * 8);
+            dst[0] = make_float4(V[k][0], V[k][1], V[k][2], V[k][3]);
+            dst[1] = make_float4(V[k][4], V[k][5], V[k][6], V[k][7]);
+        }
+    }
+}
+
 template <typename IO, int K, int M>
 int launch_typed(LatticeArgs &a, hipStream_t stream) {
     constexpr int L = lanes_for(K, M);
     constexpr int G = BLOCK / L;
     const long long groups = (a.C + G - 1) / G;
+    if constexpr (step_kernel_serves(K, M)) {
+        const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        if (a.T == 1 && a.chunks == 1 && aligned16(a.state_in) && aligned16(a.state_out)) {
+            constexpr int CPB = BLOCK / (M / 8);
+            const long long blocks = (long long)a.B * ((a.C + CPB - 1) / CPB);
+            hipLaunchKernelGGL((lattice_step_kernel<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+            return check_launch("lattice_step_kernel");
+        }
+    }
     if (a.chunks > 1) {
         // the summary: on the matrix cores for bf16 at K <= 4, M >= 32 and 16-token chunks
         bool summarised = false;

@@ -212,6 +212,26 @@ def test_decode_steps_equal_prefill(torch_mod, plugin, order, memory):
     _assert(to_numpy(state), final, "float32", "decode state")
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("order,memory", [(2, 64), (4, 32), (1, 8), (2, 128)])
+def test_decode_step_kernel(torch_mod, plugin, order, memory, dtype):
+    """T = 1 with K <= 4 and 8 <= d_m <= 128 runs the state-streaming step kernel: every dtype, a
+    partial channel group (C = 300), a masked sequence, with and without a carried-in state,
+    against the fp64 oracle on the inputs rounded to the dtype."""
+    rng = np.random.default_rng(31 + order + memory)
+    B, C = 5, 300
+    values = L.random_inputs(rng, B, 1, C, order, memory)
+    valid = np.array([True, False, True, True, False])[:, None]
+    initial = (rng.standard_normal((B, order, C, memory)) * 0.1).astype(np.float32)
+    for state in (initial, None):
+        y, final = _run(plugin, torch_mod, values, valid, state, dtype=dtype)
+        want_y, want_state = _oracle(values, valid, state, "cauchy_x_hyperbolic", dtype, torch_mod)
+        _assert(y, want_y, dtype, f"step output (state {'in' if state is not None else 'none'})")
+        _assert(final, want_state, "float32", "step state")
+        if state is not None:
+            assert np.array_equal(final[1], initial[1]) and np.array_equal(final[4], initial[4])
+
+
 def test_reference_geometry_bf16(torch_mod, plugin):
     """The reference mira-s mixer geometry (K=2, d_e=1536, d_m=16) in bf16 at 512 tokens."""
     rng = np.random.default_rng(23)
