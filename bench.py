@@ -308,12 +308,42 @@ def stack_leg(torch, steps, warmup):
     gemm_per_token = 2 * L * (d * (C + M) + d * C + d * R + R * (7 * C + 3 * M) + C * d + 2 * d * H)
     gemm_per_token += 2 * d * V
     scan_per_token = L * C * M * (9 * 2 + 4)
+    decode = decode_through_cache(torch, model, V)
     del model
     torch.cuda.empty_cache()
     return {"tokens": B * T, "forward_s": forward_s, "mixer_share": share["mixer"],
             "scan_share": share["scan"], "flops": (gemm_per_token + scan_per_token) * B * T,
             "shape": f"{L} layers, d_model {d}, d_e {C}, K 2, d_m {M}, d_r {R}, FFN {H}, "
-                     f"vocab {V}; B={B} T={T}"}
+                     f"vocab {V}; B={B} T={T}", "decode": decode}
+
+
+def decode_through_cache(torch, model, vocab, prompt=64, new=24):
+    """Greedy decoding with mira_amd.generate (the reference's mirachat.generate loop, batched):
+    a 64-token prompt, then single-token steps through the prefix cache, eager and with the step
+    replayed from a HIP graph, at batch 1 and 64. HIP events recorded as each token is accepted
+    time the steps after the first (which holds the graph capture)."""
+    from mira_amd.generate import generate
+
+    results = {}
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for batch in (1, 64):
+        ids = torch.randint(0, vocab, (batch, prompt), device="cuda", generator=g)
+        for graph in (False, True):
+            marks = []
+
+            def mark(_tokens):
+                event = torch.cuda.Event(enable_timing=True)
+                event.record()
+                marks.append(event)
+
+            generate(model, ids, 4, graph=graph)                       # warm-up
+            torch.cuda.synchronize()
+            generate(model, ids, new, graph=graph, on_token=mark)
+            torch.cuda.synchronize()
+            step_s = marks[1].elapsed_time(marks[-1]) * 1e-3 / (len(marks) - 2)
+            results[f"b{batch}_{'graph' if graph else 'eager'}"] = {
+                "tokens_per_s": round(batch / step_s, 1), "ms_per_step": round(step_s * 1e3, 3)}
+    return results
 
 
 def cpu_leg(budget_s=12.0):
@@ -451,7 +481,9 @@ def main():
             "mixer_share": round(stack["mixer_share"], 4),
             "scan_share": round(stack["scan_share"], 4),
             "tflops": round(stack["flops"] / stack["forward_s"] / 1e12, 1),
-            "flops_per_forward": stack["flops"]}
+            "flops_per_forward": stack["flops"],
+            "decode": dict(stack["decode"], metric="greedy decode through the prefix cache, "
+                                                   "64-token prompt, tokens/s per batch size")}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_leg()
     if args.calibrate:

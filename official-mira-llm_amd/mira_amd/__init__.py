@@ -7,5 +7,6 @@
   mira_amd.mixer         MiraMixer with the reference constructor and forward signature
   mira_amd.block         RMSNorm, FeedForward and MiraBlock (model/mira_block.py's API)
   mira_amd.llm           MiraLLM, the stack of blocks between the tied embedding and head
+  mira_amd.generate      decoding through the prefix cache (mirachat.generate's loop, batched)
 """
 from . import mira  # noqa: F401

@@ -82,13 +82,28 @@ class MiraMixer(nn.Module):
         return self.out_proj
 
     def project_recurrence_inputs(self, normalized_x):
-        """(input projection, coefficient projection, gamma) -- one packed GEMM for the three
-        projections of the normalised input (model/mira_mixer.py:657-712)."""
+        """(input projection, coefficient projection, gamma) of the normalised input
+        (model/mira_mixer.py:657-712). In inference the three projections run as one GEMM on a
+        packed weight kept between calls and rebuilt when any of the parameters changes (its
+        storage, version, dtype or shape), so a decode step reads the weights once instead of
+        copying them first; with gradients they run as three projections."""
         projections = (self.input_projection, self.to_gate, self.to_control)
-        weight = torch.cat([p.weight for p in projections])
-        bias = torch.cat([p.bias if p.bias is not None else p.weight.new_zeros(p.out_features)
-                          for p in projections])
-        projected = F.linear(normalized_x, weight, bias)
+        if self.training or torch.is_grad_enabled():
+            control = F.silu(self.to_control(normalized_x))
+            return (self.input_projection(normalized_x), self.coefficient_projection(control),
+                    self.to_gate(normalized_x))
+        parameters = [p.weight for p in projections] + [p.bias for p in projections
+                                                        if p.bias is not None]
+        signature = tuple((id(p), p.data_ptr(), p._version, p.dtype, p.device, tuple(p.shape))
+                          for p in parameters)
+        packed = self.__dict__.get("_packed_projection")
+        if packed is None or packed[0] != signature:
+            weight = torch.cat([p.weight for p in projections])
+            bias = torch.cat([p.bias if p.bias is not None else p.weight.new_zeros(p.out_features)
+                              for p in projections])
+            packed = (signature, weight, bias)
+            self.__dict__["_packed_projection"] = packed
+        projected = F.linear(normalized_x, packed[1], packed[2])
         projected_input, gamma, raw_control = projected.split(
             tuple(p.out_features for p in projections), dim=-1)
         control = F.silu(raw_control)
@@ -117,11 +132,18 @@ class MiraMixer(nn.Module):
         raw_rho = raw_rho.view(batch, tokens, channels, order + 1)
         memory_read = memory_read.view(batch, tokens, order + 1, memory)
         valid = None if attn_mask is None else attn_mask[:, -tokens:].bool()
-        result = plugin.matrix_lattice_iir(
-            signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
-            raw_beta=raw_beta, valid=valid,
-            state=None if cache is None else cache.get(layer),
-            return_state=cache is not None, arch=self.arch)
+        held = None if cache is None else cache.get(layer)
+        if tokens == 1 and held is not None:
+            # a decode step on a held state: updated in place, so a step allocates no state
+            # (and a captured step replays on the same tensor)
+            result = plugin.matrix_lattice_step(
+                signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
+                raw_beta, held, valid=valid, arch=self.arch, inplace=True)
+        else:
+            result = plugin.matrix_lattice_iir(
+                signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
+                raw_beta=raw_beta, valid=valid, state=held,
+                return_state=cache is not None, arch=self.arch)
         if result is None:
             raise RuntimeError(_declined(signal, order, memory))
         if cache is None:
