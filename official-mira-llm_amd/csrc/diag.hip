@@ -29,6 +29,7 @@
 #include "mira_abi_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <atomic>
 
 namespace mira {
@@ -591,7 +592,8 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
     IO *ring = static_cast<IO *>(a.ring_out);
     const long long at = (long long)b * a.D + d0;
     float xf[VEC], af[VEC], h[VEC];
-    unpack<IO>(*reinterpret_cast<const RawT *>(x + at), xf);
+    const RawT xraw = *reinterpret_cast<const RawT *>(x + at);
+    unpack<IO>(xraw, xf);
     unpack<IO>(*reinterpret_cast<const RawT *>(static_cast<const IO *>(a.a) + at), af);
     {
         const float4 v = *reinterpret_cast<const float4 *>(hstate + at);
@@ -599,9 +601,9 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
     }
     // the ring's H past tokens (slot = stream index mod H), conv weights and bias of VEC channels
     float past[VEC][H], wv[VEC][W], bias[VEC];
+    u32x2 r[3] = {};
     if constexpr (ALIGNED && sizeof(IO) == 2 && VEC * H == 12 && W == 4) {
         const unsigned *rw = reinterpret_cast<const unsigned *>(ring + at * H);
-        u32x2 r[3] = {};
         if (ring) {
 #pragma unroll
             for (int q = 0; q < 3; ++q) r[q] = reinterpret_cast<const u32x2 *>(rw)[q];
@@ -646,7 +648,34 @@ __global__ __launch_bounds__(256) void diag_step_kernel(DiagArgs a, float *hstat
         for (int j = 0; j < H; ++j) u = fmaf(wv[e][j], past[e][j], u);
         u = fmaf(wv[e][H], xf[e], u);
         h[e] = fmaf(af[e], h[e], (1.0f - af[e]) * u);
-        if (ring) ring[(at + e) * H + write_slot] = x[at + e];
+    }
+    if constexpr (ALIGNED && sizeof(IO) == 2 && VEC * H == 12 && W == 4) {
+        // the new token goes into its slot of the loaded ring words, which go back whole: three
+        // 8-byte stores per 4 channels instead of four 2-byte ones
+        if (ring) {
+            unsigned word[6] = {r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1]};
+            auto put = [&](auto slot) {
+                constexpr int S = decltype(slot)::value;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const int i = e * H + S;
+                    const unsigned half = (xraw[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                    word[i >> 1] = (i & 1) ? ((word[i >> 1] & 0xffffu) | (half << 16))
+                                           : ((word[i >> 1] & 0xffff0000u) | half);
+                }
+            };
+            if (write_slot == 0) put(std::integral_constant<int, 0>{});
+            else if (write_slot == 1) put(std::integral_constant<int, 1>{});
+            else put(std::integral_constant<int, 2>{});
+            u32x2 *dst = reinterpret_cast<u32x2 *>(ring + at * H);
+            dst[0] = u32x2{word[0], word[1]};
+            dst[1] = u32x2{word[2], word[3]};
+            dst[2] = u32x2{word[4], word[5]};
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+            if (ring) ring[(at + e) * H + write_slot] = x[at + e];
     }
     *reinterpret_cast<RawT *>(static_cast<IO *>(a.y) + at) = pack<IO>(h);
     *reinterpret_cast<float4 *>(hstate + at) = make_float4(h[0], h[1], h[2], h[3]);
