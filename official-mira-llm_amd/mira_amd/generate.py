@@ -75,6 +75,8 @@ def generate(model, prompt_ids, max_new, temperature=0.0, top_k=0, top_p=1.0, eo
     every step."""
     if prompt_ids.dim() != 2 or prompt_ids.shape[1] < 1:
         raise ValueError("prompt_ids must be [batch, tokens] with at least one token")
+    if model.training:
+        raise ValueError("generate decodes through the prefix cache, which needs model.eval()")
     batch = prompt_ids.shape[0]
     cache = PrefixCache(len(model.blocks))
     logits = model(prompt_ids, cache=cache).logits[:, -1]
