@@ -194,8 +194,7 @@ def matrix_lattice_iir(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, 
     if not status(x.device.index)[0]:
         return None
     if torch.is_grad_enabled() and any(t.requires_grad for t in tensors + (raw_beta,)):
-        if not return_state:
-            return None                      # training needs the backward, which is not built
+        return None                          # a gradient needs the backward, which is not built
     if valid is not None:
         if valid.shape != (batch, tokens) or valid.device != x.device or valid.dtype != torch.bool:
             raise ValueError("mira-dsp mask must be a boolean [batch, tokens] CUDA tensor")

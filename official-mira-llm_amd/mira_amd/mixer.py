@@ -113,6 +113,11 @@ class MiraMixer(nn.Module):
         if cache is not None and not (layer is not None and not self.training
                                       and hasattr(cache, "get")):
             raise ValueError("streaming cache is not wired into mira-dsp")
+        if torch.is_grad_enabled() and (normalized_x.requires_grad or any(
+                p.requires_grad for p in self.parameters())):
+            raise RuntimeError("the MI355X mixer serves inference only (the lattice scan has no "
+                               "backward here): run it under torch.no_grad() or "
+                               "torch.inference_mode(), or freeze its parameters")
         batch, tokens, _ = normalized_x.shape
         channels, order, memory = self.inner, self.order, self.memory_dimension
         alpha_size = channels * order

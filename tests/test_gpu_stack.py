@@ -92,3 +92,25 @@ def test_prompt_then_steps_equals_one_shot(torch_mod, model_cls):
     assert len(cache) == 26
     error = scaled(torch.cat(parts, dim=1).cpu().numpy(), full.cpu().numpy())
     assert error <= 1e-5, f"stepped vs one-shot: scaled error {error:.3e}"
+
+
+def test_gradients_are_refused_not_dropped(torch_mod, model_cls):
+    """There is no backward for the scan: under autograd the plugin declines (even with a state,
+    where the reference would return one with a gradient) and the mixer raises, instead of
+    returning values that carry no gradient."""
+    torch = torch_mod
+    from mira_amd import mira
+    from oracle import lattice as L
+
+    rng = np.random.default_rng(9)
+    values = [torch.tensor(v, device="cuda").requires_grad_() for v in L.random_inputs(rng, 1, 5, 8, 2, 16)]
+    x, alpha, rho, gamma, write, read, beta = values
+    state = torch.zeros(1, 2, 8, 16, device="cuda")
+    assert mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta, state=state,
+                                   return_state=True) is None
+    model = _model(torch, model_cls, 3, torch.float32)
+    ids = torch.tensor([[1, 2, 3]], device="cuda")
+    with pytest.raises(RuntimeError, match="inference only"):
+        model(ids)
+    with torch.no_grad():
+        assert model(ids).logits.shape == (1, 3, CFG["vocab_size"])
