@@ -85,6 +85,34 @@ int mira_lattice_step(const void *x, int64_t x_row, const void *alpha, int64_t a
                       int M, int dtype, int arch_mode, void *stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * The inference scan that forms its own coefficients from the d_r-wide control: replaces
+ * mira_fused_scan_k2_m16_r{16,32,48,64}_s{mode}_bf16 (kernel/cuda/mira_dspv2/fused_scan.cuh:259-516)
+ * as launched by matrix_lattice_iir_control (kernel/cuda/mira_dspv2/mira.py:1675-1741). Every
+ * coefficient is bf16(sum_k control[b,t,k] weight[row,k] + bias[row]), the mixer's
+ * coefficient_projection rounded once to bf16; only the order of the d_r-term sum differs from a
+ * GEMM's. The rows of weight (row stride weight_row, weight_rows rows) are
+ *   alpha of (c, k): alpha_first + c K + k;  beta: beta_first + c K + k;
+ *   rho of (c, k):   rho_first + c (K+1) + k   (k = 0..K)
+ * and bias [weight_rows] (or NULL). control [B,T,R] contiguous; the other arguments are
+ * mira_lattice_forward's, bf16 only; memory_read is the caller's projection of the control.
+ * state_in and state_out may be the same buffer. mira_lattice_control_serves says whether a call
+ * is served: bf16; (K, d_m) in {(1,8), (1,16), (2,8), (2,16), (4,8)} (the reference serves (2,16)),
+ * where it is faster than the projection GEMM plus mira_lattice_forward; R in {16,32,48,64}; and
+ * one token chunk covers the call, mira_lattice_plan_chunk(B,T,C,K,M) >= T (the reference's fused
+ * plan asks for one inference chunk, mira.py:1642-1672). A call it does not serve returns
+ * MIRA_DECLINE and the caller projects the coefficients and calls mira_lattice_forward
+ * (mira.py:1693-1704). */
+int mira_lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype);
+int mira_lattice_control_forward(const void *x, int64_t x_row, const void *control,
+                                 const void *weight, int64_t weight_row, int64_t weight_rows,
+                                 const void *bias, int64_t alpha_first, int64_t beta_first,
+                                 int64_t rho_first, const void *gamma, int64_t gamma_row,
+                                 const void *memory_write, const void *memory_read,
+                                 int64_t read_row, const uint8_t *valid, const float *state_in,
+                                 float *state_out, void *out, int B, int T, int C, int K, int M,
+                                 int R, int dtype, int arch_mode, void *stream);
+
+/* ---------------------------------------------------------------------------------------------
  * BASELINE-literal depthwise causal conv (width W) + diagonal decay scan. No reference
  * counterpart (the reference mixer has no convolution, model/prefix_cache.py:14); it is the K=1,
  * M=1 lattice after the reparameterisation r = sqrt(a^2+(1-a)^2), alpha = -atanh(a/r),

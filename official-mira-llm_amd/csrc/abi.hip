@@ -4,6 +4,7 @@
 #include "mira_device.hpp"
 #include "mira_abi_internal.hpp"
 
+#include <algorithm>
 #include <string>
 
 namespace mira {
@@ -119,6 +120,47 @@ int mira_lattice_step(const void *x, int64_t x_row, const void *alpha, int64_t a
     a.chunk = 1;
     a.chunks = 1;
     return lattice_launch(a, static_cast<hipStream_t>(stream));
+}
+
+int mira_lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype) {
+    return lattice_control_serves(B, T, C, K, M, R, dtype) ? 1 : 0;
+}
+
+int mira_lattice_control_forward(const void *x, int64_t x_row, const void *control,
+                                 const void *weight, int64_t weight_row, int64_t weight_rows,
+                                 const void *bias, int64_t alpha_first, int64_t beta_first,
+                                 int64_t rho_first, const void *gamma, int64_t gamma_row,
+                                 const void *memory_write, const void *memory_read,
+                                 int64_t read_row, const uint8_t *valid, const float *state_in,
+                                 float *state_out, void *out, int B, int T, int C, int K, int M,
+                                 int R, int dtype, int arch_mode, void *stream) {
+    if (B <= 0 || T <= 0 || C <= 0 || R <= 0)
+        return fail(MIRA_ERR_ARG, "mira: requires nonempty batch, token, channel and control axes");
+    if (!arch_valid(arch_mode)) return fail(MIRA_ERR_ARG, "mira: unknown arch mode");
+    if (!lattice_control_serves(B, T, C, K, M, R, dtype))
+        return fail(MIRA_DECLINE, "mira: the control scan serves bf16, (K, d_m) in {(1,8), (1,16), "
+                                  "(2,8), (2,16), (4,8)}, d_r in {16,32,48,64} and calls one token "
+                                  "chunk covers");
+    if (!x || !control || !weight || !gamma || !memory_write || !memory_read || !out)
+        return fail(MIRA_ERR_ARG, "mira: a required tensor is null");
+    if (x_row < C || gamma_row < C || read_row < (int64_t)(K + 1) * M || weight_row < R)
+        return fail(MIRA_DECLINE, "mira: a row stride is narrower than its row");
+    if (!aligned16(control) || (reinterpret_cast<uintptr_t>(weight) & 7u) || weight_row % 4 ||
+        (reinterpret_cast<uintptr_t>(memory_write) & 3u) ||
+        (reinterpret_cast<uintptr_t>(memory_read) & 3u) || read_row % 2)
+        return fail(MIRA_DECLINE, "mira: control must be 16-byte aligned, weight rows 8-byte "
+                                  "aligned, memory_write and memory_read rows 4-byte aligned");
+    const int64_t last = std::max({alpha_first + (int64_t)C * K, beta_first + (int64_t)C * K,
+                                   rho_first + (int64_t)C * (K + 1)});
+    if (alpha_first < 0 || beta_first < 0 || rho_first < 0 || last > weight_rows)
+        return fail(MIRA_ERR_ARG, "mira: coefficient rows fall outside the weight");
+    LatticeControlArgs a{};
+    a.x = x; a.x_row = x_row; a.control = control; a.weight = weight; a.weight_row = weight_row;
+    a.bias = bias; a.alpha_first = alpha_first; a.beta_first = beta_first; a.rho_first = rho_first;
+    a.gamma = gamma; a.gamma_row = gamma_row; a.write = memory_write; a.read = memory_read;
+    a.read_row = read_row; a.valid = valid; a.state_in = state_in; a.state_out = state_out;
+    a.out = out; a.B = B; a.T = T; a.C = C; a.K = K; a.M = M; a.R = R; a.mode = arch_mode;
+    return lattice_control_launch(a, static_cast<hipStream_t>(stream));
 }
 
 size_t mira_diag_workspace_bytes(int B, int T, int D, int dtype) {

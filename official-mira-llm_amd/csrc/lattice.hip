@@ -24,7 +24,7 @@
 // the stage coefficients r cos / r sin, x, rho and the gate: the stage maps are evaluated once per
 // channel by one thread instead of by each of the channel's L lanes, and the tile's loads are
 // issued together. Outputs of a tile leave through LDS as whole channel rows.
-#include "mira_device.hpp"
+#include "lattice_common.hpp"
 #include "mira_abi_internal.hpp"
 
 #include <algorithm>
@@ -35,49 +35,12 @@ namespace {
 
 constexpr int BLOCK = 256;
 
-__host__ __device__ constexpr int lanes_for(int K, int M) {
-    // the fewest lanes that keep a lane's share of the state at <= 32 floats
-    int L = 1;
-    while (K * M / L > 32 && L < M && L < 64) L *= 2;
-    return L;
-}
-
-// Floats of per-(token, channel) coefficients staged per token: r cos and r sin of the K stages
-// and x (summary), plus rho[K+1] and the SiLU gate (replay).
-__host__ __device__ constexpr int coef_count(int K, bool readout) {
-    return readout ? 3 * K + 3 : 2 * K + 1;
-}
-
 __host__ __device__ constexpr int tile_for(int K, int M) {
     // tokens staged per LDS tile: s and nu <= 16 KiB, the coefficient tile <= 24 KiB, <= 8 tokens
     int t = 8;
     const int G = BLOCK / lanes_for(K, M);
     while (t > 1 && (t * (K + 2) * M * 4 > 16384 || t * coef_count(K, true) * G * 4 > 24576)) t /= 2;
     return t;
-}
-
-// Memory slot of (lane, v): runs of four consecutive slots per lane (16-byte accesses) when a lane
-// owns a multiple of four slots, lane-interleaved single slots otherwise.
-template <int M, int L>
-__device__ __forceinline__ int slot(int lane, int v) {
-    constexpr int MV = M / L;
-    if constexpr (MV % 4 == 0) return ((v >> 2) * L + lane) * 4 + (v & 3);
-    else return v * L + lane;
-}
-
-// Sum over the L lanes of a channel group (adjacent lanes): cross-lane DPP within a quad,
-// then butterflies through the LDS crossbar for wider groups.
-template <int L>
-__device__ __forceinline__ float lane_sum(float v) {
-    if constexpr (L >= 2)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
-                                                                0xB1, 0xf, 0xf, false));
-    if constexpr (L >= 4)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
-                                                                0x4E, 0xf, 0xf, false));
-#pragma unroll
-    for (int offset = 4; offset < L; offset <<= 1) v += __shfl_xor(v, offset, 64);
-    return v;
 }
 
 // Stage one token tile of a channel group: per (token, channel) the stage coefficients (once per
@@ -575,42 +538,8 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
                 float y = 0.0f;
                 if (s_valid[tt]) {
                     const float *cf = s_coef + tt * NC * G + cl;
-                    float rc[K], rs[K], rho[K + 1];
-#pragma unroll
-                    for (int k = 0; k < K; ++k) { rc[k] = cf[k * G]; rs[k] = cf[(K + k) * G]; }
-                    const float xv = cf[2 * K * G];
-#pragma unroll
-                    for (int k = 0; k <= K; ++k) rho[k] = cf[(2 * K + 1 + k) * G];
-                    const float gate = cf[(3 * K + 2) * G];
-                    const float rcx = rc[K - 1] * xv;
-                    const float *nu = s_read + tt * (K + 1) * M;
-                    float acc[K + 1], sig = 0.0f;
-#pragma unroll
-                    for (int k = 0; k <= K; ++k) acc[k] = 0.0f;
-#pragma unroll
-                    for (int v = 0; v < MV; ++v) {
-                        const int m = slot<M, L>(lane, v);
-                        const float sv = s_write[tt * M + m];
-                        // stage K's level rc_K V^(K-1) + rs_K x s is only read out: its sum over m
-                        // is rc_K sum V^(K-1) nu_K + rs_K x sum s nu_K, so only U' is formed here
-                        sig = fmaf(sv, nu[K * M + m], sig);
-                        acc[K] = fmaf(V[K - 1][v], nu[K * M + m], acc[K]);
-                        float U = fmaf(rcx, sv, -(rs[K - 1] * V[K - 1][v]));
-#pragma unroll
-                        for (int k = K - 1; k >= 1; --k) {
-                            const float delayed = V[k - 1][v];
-                            const float up = rs[k - 1] * U, down = rs[k - 1] * delayed;
-                            V[k][v] = fmaf(rc[k - 1], delayed, up);        // level_k, kept
-                            U = fmaf(rc[k - 1], U, -down);
-                            acc[k] = fmaf(V[k][v], nu[k * M + m], acc[k]);
-                        }
-                        V[0][v] = U;
-                        acc[0] = fmaf(U, nu[m], acc[0]);
-                    }
-                    y = rho[K] * fmaf(rc[K - 1], acc[K], rs[K - 1] * xv * sig);
-#pragma unroll
-                    for (int k = 0; k < K; ++k) y = fmaf(rho[k], acc[k], y);
-                    y = gate * lane_sum<L>(y);
+                    y = lattice_token<K, M, L>(V, [&](int q) { return cf[q * G]; },
+                                               s_write + tt * M, s_read + tt * (K + 1) * M, lane);
                 }
                 if (lane == 0) s_out[tt * G + cl] = y;
             }

@@ -40,6 +40,25 @@ int lattice_plan_chunk(int B, int T, int C, int K, int M);
 size_t lattice_workspace(int B, int T, int C, int K, int M, int chunk);
 int lattice_launch(LatticeArgs &a, hipStream_t stream);
 
+// --- the lattice scan forming its coefficients from the control ------------------------------
+struct LatticeControlArgs {
+    const void *x;        long long x_row;
+    const void *control;                       // [B,T,R] contiguous
+    const void *weight;   long long weight_row; // coefficient_projection weight, [rows, R]
+    const void *bias;                          // [rows] or null
+    long long alpha_first, beta_first, rho_first;   // rows of alpha(c=0,k=0), beta(0,0), rho(0,0)
+    const void *gamma;    long long gamma_row;
+    const void *write;                         // [B,T,M] contiguous
+    const void *read;     long long read_row;  // [B,T,K+1,M], dense tail
+    const uint8_t *valid;                      // [B,T] or null
+    const float *state_in;                     // [B,K,C,M] or null
+    float *state_out;                          // [B,K,C,M] or null
+    void *out;                                 // [B,T,C] contiguous
+    int B, T, C, K, M, R, mode;
+};
+bool lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype);
+int lattice_control_launch(const LatticeControlArgs &a, hipStream_t stream);
+
 // --- conv + diagonal scan -------------------------------------------------------------------
 struct DiagArgs {
     const void *x;            // [B,T,D] contiguous

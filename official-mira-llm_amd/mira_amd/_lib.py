@@ -35,6 +35,10 @@ SIGNATURES = {
                               i32, i32, i32, i32, i32, i32, i32, i32, p, sz, p], i32),
     "mira_lattice_step": ([p, i64, p, i64, p, i64, p, i64, p, i64, p, p, i64, p, p, p, p,
                            i32, i32, i32, i32, i32, i32, p], i32),
+    "mira_lattice_control_serves": ([i32, i32, i32, i32, i32, i32, i32], i32),
+    "mira_lattice_control_forward": ([p, i64, p, p, i64, i64, p, i64, i64, i64, p, i64, p, p,
+                                      i64, p, p, p, p, i32, i32, i32, i32, i32, i32, i32, i32,
+                                      p], i32),
     "mira_diag_workspace_bytes": ([i32, i32, i32, i32], sz),
     "mira_diag_conv_scan": ([p, p, p, p, p, p, p, i64, p, p, i32, i32, i32, i32, i32, p, sz, p],
                             i32),

@@ -9,7 +9,8 @@ CUDA package (model/mira_mixer.py:191-218):
                                                -- mira.py:1439-1563
   matrix_lattice_iir_control(x, control, coefficient_weight, coefficient_bias, spans, gamma,
                              memory_write, valid=None, state=None, return_state=False, arch=...)
-                                               -- mira.py:1840-1894 (GEMM, then the scan)
+                                               -- mira.py:1840-1894 (coefficients formed inside
+                                                  the scan where served, else GEMM + scan)
   status(device=None) -> (bool, str)           -- mira.py:336-345
   usage() -> dict                              -- mira.py:348-349
   report(index=None)                           -- mira.py:352
@@ -45,7 +46,7 @@ ARCH_STAGE = {"cauchy_x_mobius": 3, "cauchy_x_hyperbolic": 6, "cauchy_x_identity
 DTYPE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 CONV_WIDTH = 4
 GLA_DIM = 128
-USED = {"forward": 0, "backward": 0, "step": 0, "diag": 0, "gla": 0}
+USED = {"forward": 0, "backward": 0, "step": 0, "control": 0, "diag": 0, "gla": 0}
 REPORTED = set()
 _WORKSPACES = {}
 _WORKSPACE_LOCK = threading.Lock()      # autograd / DataParallel threads may launch
@@ -267,19 +268,61 @@ def matrix_lattice_step(x, raw_alpha, raw_rho, gamma, memory_write, memory_read,
     return output, final
 
 
+def _control_plan(x, control, weight, bias, gamma, memory_write, order, memory):
+    """None, or (x row, gamma row) when the coefficient-forming scan serves this call
+    (mira.py:1642-1672): inference, bf16 throughout, a (K, d_m, d_r) the library has, one token
+    chunk, and layouts it reads in place."""
+    tensors = (x, control, weight, gamma, memory_write)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors + (bias,)
+                                       if t is not None):
+        return None
+    if not all(t.is_cuda for t in tensors) or len({t.device for t in tensors}) != 1:
+        return None
+    if any(t.dtype != torch.bfloat16 for t in tensors):
+        return None
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.device != x.device
+                             or bias.dim() != 1 or bias.stride(0) != 1):
+        return None
+    if weight.dim() != 2 or weight.stride(1) != 1 or control.dim() != 3:
+        return None
+    batch, tokens, channels = x.shape
+    rank = int(control.shape[-1])
+    if control.shape[:2] != (batch, tokens) or weight.shape[1] != rank:
+        return None
+    if not status(x.device.index)[0]:
+        return None
+    lib = _lib.require()
+    if not lib.mira_lattice_control_serves(batch, tokens, channels, order, memory, rank,
+                                           _lib.BF16):
+        return None
+    row, gamma_row = _row_stride(x, tokens), _row_stride(gamma, tokens)
+    if row is None or gamma_row is None or row < channels or gamma_row < channels:
+        return None
+    return row, gamma_row
+
+
 def matrix_lattice_iir_control(x, control, coefficient_weight, coefficient_bias, spans, gamma,
                                memory_write, valid=None, state=None, return_state=False,
                                arch="cauchy_x_hyperbolic"):
-    """The mixer forward from the d_r-wide control (mira.py:1840-1894): the coefficient
-    projection runs as one GEMM (hipBLASLt through torch), then the scan. This is the
-    reference's own fallback form (mira.py:1693-1704); the fused coefficient-forming scan is
-    not built."""
+    """The mixer forward from the d_r-wide control (mira.py:1840-1894). Where the
+    coefficient-forming scan serves the call (_control_plan) alpha, beta and rho are formed
+    inside the scan on the matrix cores from the control and coefficient_projection's rows
+    (mira_lattice_control_forward) and only memory_read is projected here; otherwise the
+    coefficient projection runs as one GEMM (hipBLASLt through torch), then the scan, bit for
+    bit the materialised path (mira.py:1693-1704)."""
     import torch.nn.functional as F
 
+    if arch not in ARCH_STAGE:
+        raise ValueError(f"arch must be one of {tuple(ARCH_STAGE)}, not {arch!r}")
     alpha_span, beta_span, rho_span, read_span = spans
     batch, tokens, channels = x.shape
     order = (alpha_span[1] - alpha_span[0]) // channels
     memory = int(memory_write.shape[-1])
+    plan = _control_plan(x, control, coefficient_weight, coefficient_bias, gamma, memory_write,
+                         order, memory)
+    if plan is not None:
+        return _control_scan(x, control, coefficient_weight, coefficient_bias, spans, gamma,
+                             memory_write, valid, state, return_state, arch, order, memory, plan)
     coefficients = F.linear(control, coefficient_weight, coefficient_bias)
     raw_alpha, raw_beta, raw_rho, memory_read = coefficients.split(
         tuple(hi - lo for lo, hi in spans), dim=-1)
@@ -289,6 +332,50 @@ def matrix_lattice_iir_control(x, control, coefficient_weight, coefficient_bias,
         memory_read.view(batch, tokens, order + 1, memory),
         raw_beta=raw_beta.view(batch, tokens, channels, order), valid=valid, state=state,
         return_state=return_state, arch=arch)
+
+
+def _control_scan(x, control, weight, bias, spans, gamma, memory_write, valid, state,
+                  return_state, arch, order, memory, plan):
+    """The coefficient-forming scan (mira.py:1705-1741): memory_read projected here, alpha, beta
+    and rho formed inside the kernel."""
+    import torch.nn.functional as F
+
+    row, gamma_row = plan
+    batch, tokens, channels = x.shape
+    (alpha_lo, alpha_hi), (beta_lo, _), (rho_lo, _), (read_lo, read_hi) = spans
+    if alpha_hi - alpha_lo != channels * order:
+        raise ValueError("mira-dsp: the alpha span must hold channels x order rows")
+    if valid is not None:
+        if valid.shape != (batch, tokens) or valid.device != x.device or valid.dtype != torch.bool:
+            raise ValueError("mira-dsp mask must be a boolean [batch, tokens] CUDA tensor")
+        valid = valid.contiguous()
+    if state is not None:
+        if (state.shape != (batch, order, channels, memory) or state.device != x.device
+                or state.dtype != torch.float32):
+            raise ValueError("mira-dsp state must be FP32 [batch, order, channels, memory]")
+        if not return_state:
+            raise ValueError("mira-dsp initial state requires return_state=True")
+        state = state.contiguous()
+    control = control.contiguous()
+    memory_write = memory_write.contiguous()
+    read_bias = None if bias is None else bias[read_lo:read_hi]
+    memory_read = F.linear(control, weight[read_lo:read_hi], read_bias).contiguous()
+    lib = _lib.require()
+    output = torch.empty(batch, tokens, channels, device=x.device, dtype=x.dtype)
+    final = (torch.empty(batch, order, channels, memory, device=x.device, dtype=torch.float32)
+             if return_state else None)
+    with torch.cuda.device(x.device):
+        code = lib.mira_lattice_control_forward(
+            _ptr(x), row, _ptr(control), _ptr(weight), int(weight.stride(0)),
+            int(weight.shape[0]), _ptr(bias), alpha_lo, beta_lo, rho_lo, _ptr(gamma), gamma_row,
+            _ptr(memory_write), _ptr(memory_read), (order + 1) * memory, _ptr(valid),
+            _ptr(state), _ptr(final), _ptr(output), batch, tokens, channels, order, memory,
+            int(control.shape[-1]), _lib.BF16, ARCH_STAGE[arch], _stream(x.device))
+    if _lib.check(code, "mira_lattice_control_forward") is None:
+        return None
+    USED["forward"] += 1
+    USED["control"] += 1
+    return (output, final) if return_state else output
 
 
 # --------------------------------------------------------------------------------------------

@@ -6,8 +6,10 @@ to_control d -> d_r, to_gate d -> d_e, coefficient_projection d_r -> alpha | bet
 (d_e K + d_e K + d_e (K+1) + (K+1) d_m), out_proj d_e -> d (no bias). The forward projects,
 splits the fused projections into strided views (no copies, model/mira_mixer.py:807-813), takes
 s = SiLU(raw write), and hands everything to mira_amd.mira.matrix_lattice_iir with the prefix
-cache's state. There is no PyTorch fallback: a declined call raises, as in the reference
-(model/mira_mixer.py:822-824).
+cache's state. An uncached, gradient-free forward hands the scan the d_r-wide control and
+coefficient_projection instead (mira_amd.mira.matrix_lattice_iir_control, which forms alpha, beta
+and rho inside the scan where it can; model/mira_mixer.py:739-760). There is no PyTorch fallback:
+a declined call raises, as in the reference (model/mira_mixer.py:822-824).
 
 The reference's lattice initializer (model/mira_initializer.py, Jeffreys-prior pole placement)
 is out of scope here; parameters use torch's default nn.Linear initialisation.
@@ -81,16 +83,18 @@ class MiraMixer(nn.Module):
     def residual_out(self):
         return self.out_proj
 
-    def project_recurrence_inputs(self, normalized_x):
-        """(input projection, coefficient projection, gamma) of the normalised input
-        (model/mira_mixer.py:657-712). In inference the three projections run as one GEMM on a
-        packed weight kept between calls and rebuilt when any of the parameters changes (its
-        storage, version, dtype or shape), so a decode step reads the weights once instead of
-        copying them first; with gradients they run as three projections."""
+    def project_recurrence_inputs(self, normalized_x, coefficients=True):
+        """(input projection, coefficient projection, gamma) of the normalised input, or with
+        coefficients=False (input projection, control, gamma) (model/mira_mixer.py:657-712). In
+        inference the three projections run as one GEMM on a packed weight kept between calls and
+        rebuilt when any of the parameters changes (its storage, version, dtype or shape), so a
+        decode step reads the weights once instead of copying them first; with gradients they
+        run as three projections."""
         projections = (self.input_projection, self.to_gate, self.to_control)
+        finish = self.coefficient_projection if coefficients else (lambda control: control)
         if self.training or torch.is_grad_enabled():
             control = F.silu(self.to_control(normalized_x))
-            return (self.input_projection(normalized_x), self.coefficient_projection(control),
+            return (self.input_projection(normalized_x), finish(control),
                     self.to_gate(normalized_x))
         parameters = [p.weight for p in projections] + [p.bias for p in projections
                                                         if p.bias is not None]
@@ -107,7 +111,17 @@ class MiraMixer(nn.Module):
         projected_input, gamma, raw_control = projected.split(
             tuple(p.out_features for p in projections), dim=-1)
         control = F.silu(raw_control)
-        return projected_input, self.coefficient_projection(control), gamma
+        return projected_input, finish(control), gamma
+
+    def _forms_coefficients_in_scan(self, normalized_x, cache):
+        """Whether this call takes the coefficient-forming scan (model/mira_mixer.py:739-760):
+        an uncached, gradient-free forward whose coefficient_projection is a plain, unhooked
+        nn.Linear, and no positive-pole remapping."""
+        projection = self.coefficient_projection
+        return (normalized_x.is_cuda and cache is None and not self.positive_poles
+                and not torch.is_grad_enabled() and type(projection) is nn.Linear
+                and not projection._forward_pre_hooks and not projection._forward_hooks
+                and "forward" not in projection.__dict__)
 
     def forward(self, normalized_x, attn_mask=None, cache=None, layer=None):
         if cache is not None and not (layer is not None and not self.training
@@ -120,6 +134,22 @@ class MiraMixer(nn.Module):
                                "torch.inference_mode(), or freeze its parameters")
         batch, tokens, _ = normalized_x.shape
         channels, order, memory = self.inner, self.order, self.memory_dimension
+        if self._forms_coefficients_in_scan(normalized_x, cache):
+            input_projection, control, gamma = self.project_recurrence_inputs(
+                normalized_x, coefficients=False)
+            signal, raw_write = input_projection.split((channels, memory), dim=-1)
+            valid = None if attn_mask is None else attn_mask[:, -tokens:].bool()
+            projection = self.coefficient_projection
+            mixed = plugin.matrix_lattice_iir_control(
+                signal, control, projection.weight, projection.bias,
+                (self.alpha_span, self.beta_span, self.rho_span, self.read_span), gamma,
+                F.silu(raw_write).contiguous(), valid=valid, arch=self.arch)
+            if mixed is None:
+                raise RuntimeError(_declined(signal, order, memory))
+            output = self.out_proj(self.dropout(mixed))
+            if valid is not None:
+                output = torch.where(valid.unsqueeze(-1), output, torch.zeros_like(output))
+            return output
         alpha_size = channels * order
         rho_size = channels * (order + 1)
         read_size = (order + 1) * memory

@@ -89,3 +89,35 @@ def test_argument_errors_without_a_launch(lib):
                                    1, 8, 6, 4, 1, fake, 1 << 20, null) == 1
     # gla: d = 64 declines
     assert lib.mira_gla_step(fake, fake, fake, fake, fake, fake, 1, 1, 64, 64, 1, null) == 1
+
+
+def test_control_scan_plan_and_errors(lib):
+    """mira_lattice_control_serves: bf16, the (K, d_m) where forming the coefficients in the scan
+    is the faster path, d_r in {16, 32, 48, 64}, one token chunk; anything else declines before
+    any HIP call, and coefficient rows outside the weight are a bad argument."""
+    bf16, f32 = 1, 0
+    served = {(1, 8), (1, 16), (2, 8), (2, 16), (4, 8)}
+    for K in (1, 2, 4, 8):
+        for M in (8, 16, 32, 64):
+            want = int((K, M) in served)
+            assert lib.mira_lattice_control_serves(8, 16, 256, K, M, 48, bf16) == want, (K, M)
+    assert lib.mira_lattice_control_serves(8, 16, 256, 2, 16, 48, f32) == 0
+    for rank in (8, 24, 80, 128):
+        assert lib.mira_lattice_control_serves(8, 16, 256, 2, 16, rank, bf16) == 0
+    # a call the chunk planner would split (one sequence of 300 tokens) declines
+    assert lib.mira_lattice_plan_chunk(1, 300, 1536, 2, 16) < 300
+    assert lib.mira_lattice_control_serves(1, 300, 1536, 2, 16, 48, bf16) == 0
+    assert lib.mira_lattice_control_serves(1, 16, 1536, 2, 16, 48, bf16) == 1
+    null, fake = None, ctypes.c_void_p(256)
+    C, K, M, R = 32, 2, 16, 48
+    rows = C * (3 * K + 1) + (K + 1) * M
+
+    def call(alpha_first=0, weight_rows=rows, dtype=bf16, order=K):
+        return lib.mira_lattice_control_forward(
+            fake, C, fake, fake, R, weight_rows, null, alpha_first, C * K, 2 * C * K, fake, C,
+            fake, fake, (K + 1) * M, null, null, null, fake, 2, 4, C, order, M, R, dtype, 6, null)
+
+    assert call(dtype=f32) == 1
+    assert call(order=8) == 1
+    assert call(alpha_first=-1) == 2
+    assert call(weight_rows=2 * C * K) == 2 and b"outside the weight" in lib.mira_last_error()

@@ -1,0 +1,199 @@
+"""GPU parity of the coefficient-forming scan (mira_lattice_control_forward, reached through
+matrix_lattice_iir_control) against the materialised path (F.linear, then the lattice scan) and
+the oracle.
+
+Follows the reference harness's fused-scan check (kernel/cuda/mira_dspv2/check.py:1130-1261):
+the same generators (weight ~ N(0, 1/d_r), bias ~ 0.3 N(0, 1), control = SiLU(N(0, 1)), x and
+gamma as strided views of one packed tensor, write ~ N(0, 1)/4), the same bound (scaled error
+<= 2e-2 against both the materialised path and the float reference, with at most 2 % of the bf16
+outputs differing from the materialised path's: a formed coefficient may land one bf16 ulp away
+because its d_r-term sum runs in another order), a split sequence that falls back to the
+materialised path bit for bit, every stage map, and the mixer's eval forward. The reference's
+shapes are kept where this library serves them in one token chunk; B=64 T=257 (chunked here)
+becomes B=192 T=257.
+"""
+import numpy as np
+import pytest
+
+from _util import HALF_SCALED, scaled, to_numpy
+from oracle import lattice as L
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "the gpu tests need a HIP device"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def plugin():
+    from mira_amd import _lib, mira
+
+    assert _lib.library() is not None, _lib.why()
+    return mira
+
+
+def _inputs(torch, batch, tokens, channels, rank, order, memory, masked, with_state, seed):
+    generator = torch.Generator(device="cuda").manual_seed(seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, device="cuda", generator=generator)
+
+    total = channels * (3 * order + 1) + (order + 1) * memory
+    spans = ((0, channels * order), (channels * order, 2 * channels * order),
+             (2 * channels * order, channels * (3 * order + 1)), (channels * (3 * order + 1), total))
+    weight = (randn(total, rank) / rank ** 0.5).to(torch.bfloat16)
+    bias = (0.3 * randn(total)).to(torch.bfloat16)
+    control = torch.nn.functional.silu(randn(batch, tokens, rank)).to(torch.bfloat16)
+    packed = randn(batch, tokens, 2 * channels + 3).to(torch.bfloat16)
+    signal, gamma = packed[..., :channels], packed[..., channels:2 * channels]
+    write = (randn(batch, tokens, memory) / 4).to(torch.bfloat16)
+    valid = (torch.rand(batch, tokens, device="cuda", generator=generator) > 0.25) if masked else None
+    state = randn(batch, order, channels, memory) if with_state else None
+    return dict(weight=weight, bias=bias, control=control, signal=signal, gamma=gamma,
+                write=write, valid=valid, state=state, spans=spans)
+
+
+def _materialised(plugin, torch, v, order, memory, arch, with_state):
+    import torch.nn.functional as F
+
+    batch, tokens, channels = v["signal"].shape
+    coefficients = F.linear(v["control"], v["weight"], v["bias"])
+    alpha, beta, rho, read = coefficients.split(tuple(hi - lo for lo, hi in v["spans"]), dim=-1)
+    views = (alpha.view(batch, tokens, channels, order), rho.view(batch, tokens, channels, order + 1),
+             read.view(batch, tokens, order + 1, memory), beta.view(batch, tokens, channels, order))
+    out = plugin.matrix_lattice_iir(
+        v["signal"], views[0], views[1], v["gamma"], v["write"], views[2], raw_beta=views[3],
+        valid=v["valid"], state=v["state"], return_state=with_state, arch=arch)
+    return out, views
+
+
+def _case(plugin, torch, batch, tokens, channels, rank, masked=False, with_state=False,
+          arch="cauchy_x_mobius", order=2, memory=16, expect_fused=True, oracle=True, seed=0):
+    torch.manual_seed(20261011 + batch + tokens + channels + rank)
+    v = _inputs(torch, batch, tokens, channels, rank, order, memory, masked, with_state,
+                20261011 + batch + tokens + channels + rank + seed)
+    before = plugin.usage()["control"]
+    with torch.no_grad():
+        got = plugin.matrix_lattice_iir_control(
+            v["signal"], v["control"], v["weight"], v["bias"], v["spans"], v["gamma"], v["write"],
+            valid=v["valid"], state=v["state"], return_state=with_state, arch=arch)
+        fused = plugin.usage()["control"] > before
+        want, views = _materialised(plugin, torch, v, order, memory, arch, with_state)
+    assert got is not None and want is not None
+    assert fused == expect_fused, f"fused path taken: {fused}, expected {expect_fused}"
+    if with_state:
+        (got, got_final), (want, want_final) = got, want
+    torch.cuda.synchronize()
+    if not expect_fused:
+        assert torch.equal(got, want), "the fallback must be the materialised path bit for bit"
+        if with_state:
+            assert torch.equal(got_final, want_final)
+        return 0.0, 0.0
+    differing = float((got != want).float().mean())
+    error = scaled(to_numpy(got), to_numpy(want))
+    if oracle:
+        seen = [to_numpy(t) for t in (v["signal"], views[0], views[1], v["gamma"], v["write"],
+                                      views[2], views[3])]
+        exact, exact_final = L.lattice_scan_sequential(
+            *seen, valid=None if v["valid"] is None else to_numpy(v["valid"]).astype(bool),
+            state=None if v["state"] is None else to_numpy(v["state"]), arch=arch,
+            dtype=np.float64)
+        error = max(error, scaled(to_numpy(got), exact))
+        if with_state:
+            error = max(error, scaled(to_numpy(got_final), exact_final))
+    elif with_state:
+        error = max(error, scaled(to_numpy(got_final), to_numpy(want_final)))
+    assert error <= HALF_SCALED and differing <= 0.02, (
+        f"B={batch} T={tokens} C={channels} d_r={rank} {arch}: scaled error {error:.3e}, "
+        f"{differing:.2%} of outputs differ from the materialised path")
+    return error, differing
+
+
+@pytest.mark.parametrize("args", [
+    (19, 5, 70, 48, False, False, "cauchy_x_mobius"),
+    (19, 5, 70, 48, True, True, "cauchy_x_mobius"),
+    (3, 4, 32, 16, True, False, "cauchy_x_hyperbolic"),
+    (17, 3, 40, 32, False, True, "cauchy_x_identity"),
+    (5, 16, 64, 64, True, True, "gaussian_x_mobius"),
+], ids=lambda a: f"B{a[0]}T{a[1]}C{a[2]}r{a[3]}{'m' if a[4] else ''}{'s' if a[5] else ''}")
+def test_reference_cases(torch_mod, plugin, args):
+    _case(plugin, torch_mod, *args)
+
+
+@pytest.mark.parametrize("args", [(192, 257, 1536, 48, False, False, "cauchy_x_mobius"),
+                                  (571, 33, 1536, 48, True, False, "cauchy_x_mobius")],
+                         ids=["B192T257", "B571T33"])
+def test_reference_geometry_at_batch(torch_mod, plugin, args):
+    """The reference mira-s geometry (d_e 1536, d_m 16, d_r 48) at batches that fill the GPU
+    in one token chunk: against the materialised path (the float oracle would take minutes)."""
+    _case(plugin, torch_mod, *args, oracle=False)
+
+
+@pytest.mark.parametrize("number,arch", list(enumerate(L.ARCH_STAGE)))
+def test_every_arch(torch_mod, plugin, number, arch):
+    rank = (16, 32, 48, 64)[number % 4]
+    _case(plugin, torch_mod, 6 + number, 3 + number % 5, 64 + 32 * (number % 3), rank,
+          number % 2 == 1, number % 3 == 0, arch)
+
+
+@pytest.mark.parametrize("order,memory", [(1, 8), (1, 16), (2, 8), (4, 8)])
+def test_orders_and_memories(torch_mod, plugin, order, memory):
+    """The other served shapes beside the reference's one (K=2, d_m=16)."""
+    _case(plugin, torch_mod, 9, 11, 48, 32, True, True, "cauchy_x_hyperbolic", order=order,
+          memory=memory)
+
+
+@pytest.mark.parametrize("order,memory", [(1, 32), (2, 32), (2, 64), (4, 16)])
+def test_unserved_shapes_fall_back(torch_mod, plugin, order, memory):
+    """(K, d_m) where the materialised path is the faster one: bit for bit that path."""
+    _case(plugin, torch_mod, 9, 11, 48, 32, True, True, "cauchy_x_hyperbolic", order=order,
+          memory=memory, expect_fused=False)
+
+
+def test_split_sequence_falls_back_bit_for_bit(torch_mod, plugin):
+    _case(plugin, torch_mod, 1, 300, 1536, 48, expect_fused=False)
+
+
+def test_unserved_rank_falls_back(torch_mod, plugin):
+    _case(plugin, torch_mod, 4, 6, 64, 128, expect_fused=False)
+
+
+def test_errors(torch_mod, plugin):
+    torch = torch_mod
+    v = _inputs(torch, 2, 3, 32, 16, 2, 16, False, False, 5)
+    args = (v["signal"], v["control"], v["weight"], v["bias"], v["spans"], v["gamma"], v["write"])
+    with torch.no_grad():
+        with pytest.raises(ValueError):
+            plugin.matrix_lattice_iir_control(*args, state=torch.zeros(2, 2, 32, 16, device="cuda"))
+        with pytest.raises(ValueError):
+            plugin.matrix_lattice_iir_control(*args, valid=torch.ones(2, 3, device="cuda"))
+
+
+def test_mixer_eval_forward_takes_the_control_scan(torch_mod, plugin):
+    """model/mira_mixer.py routes an uncached eval forward through matrix_lattice_iir_control; a
+    forward hook on coefficient_projection sends it down the materialised path instead, as in
+    the reference (model/mira_mixer.py:749-752)."""
+    torch = torch_mod
+    from mira_amd.mixer import MiraMixer
+
+    torch.manual_seed(3)
+    mixer = MiraMixer(768, lattice_order=2, d_e=1536, coefficient_bottleneck=48,
+                      memory_dimension=16).cuda().to(torch.bfloat16).eval()
+    x = torch.randn(8, 16, 768, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        before = plugin.usage()["control"]
+        fused = mixer(x)
+        assert plugin.usage()["control"] == before + 1, "the mixer did not reach the control scan"
+        handle = mixer.coefficient_projection.register_forward_hook(lambda *a: None)
+        try:
+            plain = mixer(x)
+        finally:
+            handle.remove()
+        assert plugin.usage()["control"] == before + 1
+    error = scaled(to_numpy(fused), to_numpy(plain))
+    assert error <= HALF_SCALED, f"fused vs materialised mixer forward: {error:.3e}"
