@@ -10,8 +10,10 @@ tokens/s over exactly K timed steps. Beside it: the decode leg (`configs[3]`, ba
 HIP events on the launch stream, and the CPU oracle timed on the host's cores on a bounded
 sample of the same workload. Also reported, not headline: the GLA chunked prefill (`configs[2]`,
 % HBM and % MFMA), the reference operator matrix_lattice_iir at the cfg5 mixer geometry
-(K=2, M=64), and the 24-layer MiraLLM forward of `configs[4]` with the mixer's and the scan's
-share of its time (skip it with --no-stack). Prints one JSON line.
+(K=2, M=64), matrix_lattice_iir_control (coefficients formed inside the scan) at the
+reference's own mixer geometry against its materialised path, and the 24-layer MiraLLM forward
+of `configs[4]` with the mixer's and the scan's share of its time (skip it with --no-stack).
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -235,6 +237,78 @@ def lattice_leg(torch, mira, steps, warmup):
             "step_bytes": step_bytes, "step_shape": f"B={SB} T=1 C={C} K={K} M={M}"}
 
 
+def control_leg(torch, mira, steps, warmup):
+    """matrix_lattice_iir_control (mira.py:1840-1894) at the reference's own mixer geometry
+    (K=2, d_e 1536, d_m 16, d_r 48, cauchy_x_hyperbolic) at a batch that fills the GPU in one
+    token chunk, B=256 T=512: the scan forms alpha, beta and rho from the control on the matrix
+    cores, against the materialised path (the coefficient GEMM, then matrix_lattice_iir) on the
+    same inputs. The kernel alone is also timed through the C-ABI, with memory_read projected
+    beforehand. Algorithmic bytes of the kernel: x, gamma, y 6 B per (t,c) + control 2 d_r + s,
+    nu 2 (K+2) M per token; fp32 VALU flops B*T*C*M*(9K+4)."""
+    import torch.nn.functional as F
+
+    from mira_amd import _lib
+
+    B, T, C, K, M, R = 256, 512, 1536, 2, 16, 48
+    arch = "cauchy_x_hyperbolic"
+    g = torch.Generator(device="cuda").manual_seed(8)
+    bf = torch.bfloat16
+    total = C * (3 * K + 1) + (K + 1) * M
+    spans = ((0, C * K), (C * K, 2 * C * K), (2 * C * K, C * (3 * K + 1)), (C * (3 * K + 1), total))
+    weight = (torch.randn(total, R, device="cuda", generator=g) / R ** 0.5).to(bf)
+    bias = (0.3 * torch.randn(total, device="cuda", generator=g)).to(bf)
+    control = F.silu(torch.randn(B, T, R, device="cuda", generator=g)).to(bf)
+    packed = torch.randn(B, T, 2 * C, device="cuda", generator=g).to(bf)
+    x, gamma = packed[..., :C], packed[..., C:]
+    write = (torch.randn(B, T, M, device="cuda", generator=g) / 4).to(bf)
+    read = F.linear(control, weight[spans[3][0]:], bias[spans[3][0]:]).contiguous()
+    plan = mira._control_plan(x, control, weight, bias, gamma, write, K, M)
+    assert plan is not None, "the control scan does not serve the bench shape"
+    lib = _lib.require()
+    out = torch.empty(B, T, C, device="cuda", dtype=bf)
+    stream = torch.cuda.current_stream()
+
+    def fused():
+        return mira.matrix_lattice_iir_control(x, control, weight, bias, spans, gamma, write,
+                                               arch=arch)
+
+    def kernel():
+        lib.mira_lattice_control_forward(
+            x.data_ptr(), plan[0], control.data_ptr(), weight.data_ptr(), R, total,
+            bias.data_ptr(), spans[0][0], spans[1][0], spans[2][0], gamma.data_ptr(), plan[1],
+            write.data_ptr(), read.data_ptr(), (K + 1) * M, None, None, None, out.data_ptr(),
+            B, T, C, K, M, R, _lib.BF16, mira.ARCH_STAGE[arch], stream.cuda_stream)
+
+    def materialised():
+        coefficients = F.linear(control, weight, bias)
+        alpha, beta, rho, nu = coefficients.split(tuple(hi - lo for lo, hi in spans), dim=-1)
+        return mira.matrix_lattice_iir(
+            x, alpha.view(B, T, C, K), rho.view(B, T, C, K + 1), gamma, write,
+            nu.view(B, T, K + 1, M), raw_beta=beta.view(B, T, C, K), arch=arch)
+
+    def timed(fn):
+        with torch.no_grad():
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            end.record(stream)
+            torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e-3 / steps
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            fused(), kernel(), materialised()
+    call_s, kernel_s, materialised_s = timed(fused), timed(kernel), timed(materialised)
+    with torch.no_grad():
+        same = float((fused() == materialised()).float().mean())
+    nbytes = B * T * C * 6 + B * T * (2 * R + 2 * (K + 2) * M)
+    return {"tokens": B * T, "call_s": call_s, "kernel_s": kernel_s,
+            "materialised_s": materialised_s, "bytes": nbytes, "flops": B * T * C * M * (9 * K + 4),
+            "identical": same, "shape": f"B={B} T={T} C={C} K={K} M={M} d_r={R}"}
+
+
 def stack_leg(torch, steps, warmup):
     """24 random-init MiraBlocks (d_model 2048, lattice_d_e 2048, K=2,
     d_m 64, d_r 128, FFN 8192 SiLU-MLP), vocab 32000 with the tied head, weights N(0, 0.02^2),
@@ -400,6 +474,7 @@ def main():
     gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3)
     gla_hbm = gla["algorithmic"] / gla["kernel_s"] / 1e9
     lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2)
+    ctl = control_leg(torch, mira, max(5, args.steps // 10), 3)
     stack = None if args.no_stack else stack_leg(torch, 3, 1)
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
     traffic = traffic_from_profiles("diag_column_kernel")
@@ -470,6 +545,24 @@ def main():
                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(lat["step_bytes"] / lat["step_s"] / 1e9 / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": lat["step_bytes"]}}},
+        "control_scan": {
+            "metric": "matrix_lattice_iir_control tokens/s at the reference mixer geometry, bf16, "
+                      "coefficients formed inside the scan",
+            "shape": ctl["shape"], "unit": "tokens/s", "value": ctl["tokens"] / ctl["call_s"],
+            "call_us": round(ctl["call_s"] * 1e6, 1),
+            "kernel": "lattice_control_kernel", "kernel_us": round(ctl["kernel_s"] * 1e6, 1),
+            "materialised_value": ctl["tokens"] / ctl["materialised_s"],
+            "materialised_us": round(ctl["materialised_s"] * 1e6, 1),
+            "speedup": round(ctl["materialised_s"] / ctl["call_s"], 3),
+            "outputs_identical_to_materialised": round(ctl["identical"], 6),
+            "hbm": {"achieved": round(ctl["bytes"] / ctl["kernel_s"] / 1e9, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ctl["bytes"] / ctl["kernel_s"] / 1e9 / HBM_PEAK_GBS, 4),
+                    "algorithmic_bytes": ctl["bytes"]},
+            "valu": {"achieved": round(ctl["flops"] / ctl["kernel_s"] / 1e12, 1),
+                     "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(ctl["flops"] / ctl["kernel_s"] / 1e12 / 157.3, 4),
+                     "flops": ctl["flops"]}},
         "watchdog": prefill["watchdog"],
     }
     if stack is not None:

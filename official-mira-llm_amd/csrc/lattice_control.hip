@@ -91,9 +91,15 @@ __global__ __launch_bounds__(THREADS) void lattice_control_kernel(LatticeControl
     __shared__ uint16_t s_out[2][ROWS][G];
     __shared__ unsigned char s_valid[2][ROWS];
 
+    // Workgroups go round-robin over the 8 XCDs, each with its own L2: block i runs logical block
+    // (i % 8) (n / 8) + i / 8, so an XCD takes a contiguous run of channel groups of one batch
+    // group -- the groups sharing a 128-byte line of x, gamma and y, and the batch group's control
+    // and s rows, meet in one L2.
+    const int n_blocks = gridDim.x, i_block = blockIdx.x;
+    const int logical = n_blocks % 8 ? i_block : (i_block % 8) * (n_blocks / 8) + i_block / 8;
     // row r of a tile is token n TT + r / SB of sequence b0 + r % SB
     const int groups = (a.C + G - 1) / G;
-    const int c0 = (blockIdx.x % groups) * G, b0 = (blockIdx.x / groups) * SB;
+    const int c0 = (logical % groups) * G, b0 = (logical / groups) * SB;
     const int tid = threadIdx.x, wave = tid >> 6, wl = tid & 63;
     const int lane = tid % L, cl = (tid / L) % G, sb = tid / (L * G);
     const int b = b0 + sb, c = c0 + cl;
