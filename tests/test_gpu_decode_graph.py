@@ -27,7 +27,10 @@ def plugin():
     return mira
 
 
-def test_decode_steps_replayed_from_a_graph(torch_mod, plugin):
+@pytest.mark.parametrize("overlap", [False, True], ids=["one_stream", "side_stream"])
+def test_decode_steps_replayed_from_a_graph(torch_mod, plugin, overlap):
+    """With overlap, each step's conv + diagonal launch goes to a side stream forked from the
+    main stream and joined before the next step (the decode bench's launch scheme)."""
     torch = torch_mod
     B, D, H, d, N = 8, 256, 2, 128, 6
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -50,6 +53,15 @@ def test_decode_steps_replayed_from_a_graph(torch_mod, plugin):
             plugin.diag_conv_step(xs[t], as_[t], w, bias, h, ring, pos=t, out=ys[t])
             plugin.gla_step(qs[t], ks[t], vs[t], gs[t], S, out=os_[t])
 
+    def run_overlapped(h, ring, S, ys, os_):
+        main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+        for t in range(N):
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                plugin.diag_conv_step(xs[t], as_[t], w, bias, h, ring, pos=t, out=ys[t])
+            plugin.gla_step(qs[t], ks[t], vs[t], gs[t], S, out=os_[t])
+            main.wait_stream(side)
+
     he, re, Se = h0.clone(), ring0.clone(), S0.clone()
     ye, oe = torch.empty(N, B, D, device="cuda", dtype=bf), torch.empty(N, B, H, d, device="cuda", dtype=bf)
     run(he, re, Se, ye, oe)
@@ -59,7 +71,7 @@ def test_decode_steps_replayed_from_a_graph(torch_mod, plugin):
     yg, og = torch.empty_like(ye), torch.empty_like(oe)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        run(hg, rg, Sg, yg, og)
+        (run_overlapped if overlap else run)(hg, rg, Sg, yg, og)
     for replay in range(3):
         hg.copy_(h0)
         rg.copy_(ring0)
