@@ -155,6 +155,28 @@ def test_unserved_shapes_fall_back(torch_mod, plugin, order, memory):
           memory=memory, expect_fused=False)
 
 
+@pytest.mark.parametrize("args", [(64, 1, 64, 48, True, True), (40, 2, 96, 32, False, True)],
+                         ids=["one_token", "two_tokens"])
+def test_short_calls(torch_mod, plugin, args):
+    """A single token (a cached step's shape) and two tokens, with carried state."""
+    _case(plugin, torch_mod, *args, arch="cauchy_x_hyperbolic")
+
+
+def test_fully_masked_rows_keep_the_state(torch_mod, plugin):
+    """A sequence whose every token is masked writes zeros and hands its state back unchanged."""
+    torch = torch_mod
+    B, T, C, K, M, R = 6, 9, 48, 2, 16, 32
+    v = _inputs(torch, B, T, C, R, K, M, True, True, 11)
+    v["valid"][2] = False
+    with torch.no_grad():
+        out, final = plugin.matrix_lattice_iir_control(
+            v["signal"], v["control"], v["weight"], v["bias"], v["spans"], v["gamma"], v["write"],
+            valid=v["valid"], state=v["state"], return_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out[2], torch.zeros_like(out[2]))
+    assert torch.equal(final[2], v["state"][2])
+
+
 def test_split_sequence_falls_back_bit_for_bit(torch_mod, plugin):
     _case(plugin, torch_mod, 1, 300, 1536, 48, expect_fused=False)
 
