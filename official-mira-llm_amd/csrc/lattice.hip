@@ -46,12 +46,14 @@ __host__ __device__ constexpr int tile_for(int K, int M) {
 // Stage one token tile of a channel group: per (token, channel) the stage coefficients (once per
 // channel, not once per lane), x, and for the readout rho and the gate; per token the valid flag.
 // Layout coef[token][quantity][channel] so that a wave's reads of one quantity are contiguous.
-template <typename IO, int K, bool READOUT>
+// MODE is the stage mode when the kernel is built for one stage map, 0 when it reads a.mode.
+template <typename IO, int K, bool READOUT, int MODE = 0>
 __device__ __forceinline__ void stage_coefficient_tile(const LatticeArgs &a, int b, int tile, int n,
                                                        int c0, int G, float *coef,
                                                        unsigned char *valid) {
     constexpr int NC = coef_count(K, READOUT);
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    const int mode = MODE ? MODE : a.mode;
+    const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
     for (int i = threadIdx.x; i < n * G; i += BLOCK) {
         const int tt = i / G, cl = i % G, c = c0 + cl;
         float *dst = coef + tt * NC * G + cl;
@@ -229,7 +231,7 @@ __device__ __forceinline__ void suffix_round(float (&X)[K][K]) {
 }
 }  // namespace summary_mfma
 
-template <int K, int M>
+template <int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     using namespace summary_mfma;
     constexpr int G = ROWS / K;                  // channels per block
@@ -250,7 +252,8 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int t = tid & (TT - 1), row = tid / TT;
     const int c0 = group * G, cr = c0 + row * CP;    // this lane's first channel
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    const int mode = MODE ? MODE : a.mode;
+    const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
 
     __shared__ alignas(16) uint16_t s_wT[M][TP];  // s^T of the tile, [m][token]
     __shared__ alignas(16) uint16_t s_hi[ROWS][TP], s_lo[ROWS][TP];   // g, [(c, k)][token]
@@ -479,7 +482,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_combine(LatticeArgs a) {
 // ---------------------------------------------------------------------------------------------
 // replay: the scan of one chunk from its entering state, with readout and gate
 // ---------------------------------------------------------------------------------------------
-template <typename IO, int K, int M>
+template <typename IO, int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     constexpr int L = lanes_for(K, M);
     constexpr int G = BLOCK / L;
@@ -531,7 +534,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
             const int tt = i / ((K + 1) * M), rest = i % ((K + 1) * M);
             s_read[i] = load(read + ((long long)b * a.T + tile + tt) * a.read_row + rest);
         }
-        stage_coefficient_tile<IO, K, true>(a, b, tile, n, group * G, G, s_coef, s_valid);
+        stage_coefficient_tile<IO, K, true, MODE>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
         if (active) {
             for (int tt = 0; tt < n; ++tt) {
@@ -673,20 +676,12 @@ __global__ __launch_bounds__(BLOCK) void lattice_step_kernel(LatticeArgs a) {
     }
 }
 
-template <typename IO, int K, int M>
-int launch_typed(LatticeArgs &a, hipStream_t stream) {
+// The chunked path (summary, combine, replay) with the stage map compiled in when MODE != 0.
+template <typename IO, int K, int M, int MODE>
+int launch_chunked(LatticeArgs &a, hipStream_t stream) {
     constexpr int L = lanes_for(K, M);
     constexpr int G = BLOCK / L;
     const long long groups = (a.C + G - 1) / G;
-    if constexpr (step_kernel_serves(K, M)) {
-        const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-        if (a.T == 1 && a.chunks == 1 && aligned16(a.state_in) && aligned16(a.state_out)) {
-            constexpr int CPB = BLOCK / (M / 8);
-            const long long blocks = (long long)a.B * ((a.C + CPB - 1) / CPB);
-            hipLaunchKernelGGL((lattice_step_kernel<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
-            return check_launch("lattice_step_kernel");
-        }
-    }
     if (a.chunks > 1) {
         // the summary: on the matrix cores for bf16 at K <= 4, M >= 32 and 16-token chunks
         bool summarised = false;
@@ -694,7 +689,8 @@ int launch_typed(LatticeArgs &a, hipStream_t stream) {
             if (a.chunk % summary_mfma::TT == 0) {
                 constexpr int GM = summary_mfma::ROWS / K;
                 const long long blocks = (long long)a.B * (a.chunks - 1) * ((a.C + GM - 1) / GM);
-                hipLaunchKernelGGL((lattice_summary_mfma<K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+                hipLaunchKernelGGL((lattice_summary_mfma<K, M, MODE>), dim3(blocks), dim3(BLOCK), 0,
+                                   stream, a);
                 if (int rc = check_launch("lattice_summary_mfma")) return rc;
                 summarised = true;
             }
@@ -710,8 +706,48 @@ int launch_typed(LatticeArgs &a, hipStream_t stream) {
         if (int rc = check_launch("lattice_combine")) return rc;
     }
     const long long blocks = (long long)a.B * a.chunks * groups;
-    hipLaunchKernelGGL((lattice_replay<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+    hipLaunchKernelGGL((lattice_replay<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0, stream, a);
     return check_launch("lattice_replay");
+}
+
+// bf16 at the mixer's shapes runs summary and replay kernels built for their one stage map: the
+// fifteen maps and the branches between them in one kernel cost 9-30 % (replay at K = 2, d_m = 64
+// and 16) and 10 % (summary) against kernels that carry one map.
+__host__ __device__ constexpr bool fixed_stage_map(int K, int M) {
+    return (K == 1 || K == 2 || K == 4) && (M == 16 || M == 32 || M == 64 || M == 128);
+}
+
+template <typename IO, int K, int M>
+int launch_typed(LatticeArgs &a, hipStream_t stream) {
+    if constexpr (step_kernel_serves(K, M)) {
+        const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        if (a.T == 1 && a.chunks == 1 && aligned16(a.state_in) && aligned16(a.state_out)) {
+            constexpr int CPB = BLOCK / (M / 8);
+            const long long blocks = (long long)a.B * ((a.C + CPB - 1) / CPB);
+            hipLaunchKernelGGL((lattice_step_kernel<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+            return check_launch("lattice_step_kernel");
+        }
+    }
+    if constexpr (std::is_same<IO, bf16_t>::value && fixed_stage_map(K, M)) {
+        switch (a.mode) {
+            case 3: return launch_chunked<IO, K, M, 3>(a, stream);
+            case 6: return launch_chunked<IO, K, M, 6>(a, stream);
+            case 7: return launch_chunked<IO, K, M, 7>(a, stream);
+            case 8: return launch_chunked<IO, K, M, 8>(a, stream);
+            case 9: return launch_chunked<IO, K, M, 9>(a, stream);
+            case 10: return launch_chunked<IO, K, M, 10>(a, stream);
+            case 11: return launch_chunked<IO, K, M, 11>(a, stream);
+            case 12: return launch_chunked<IO, K, M, 12>(a, stream);
+            case 13: return launch_chunked<IO, K, M, 13>(a, stream);
+            case 14: return launch_chunked<IO, K, M, 14>(a, stream);
+            case 15: return launch_chunked<IO, K, M, 15>(a, stream);
+            case 16: return launch_chunked<IO, K, M, 16>(a, stream);
+            case 17: return launch_chunked<IO, K, M, 17>(a, stream);
+            case 18: return launch_chunked<IO, K, M, 18>(a, stream);
+            case 19: return launch_chunked<IO, K, M, 19>(a, stream);
+        }
+    }
+    return launch_chunked<IO, K, M, 0>(a, stream);
 }
 
 template <typename IO, int K>

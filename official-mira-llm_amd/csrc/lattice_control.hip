@@ -45,11 +45,11 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // The (K, d_m) served: one lane holds a whole stream (K d_m <= 32) and the scan's work per
 // (token, channel) is small next to the 3K + 1 coefficients it saves reading. Measured against
-// the projection GEMM plus the replay at B256 T512 C1536: 1.31x (1, 8), 1.08x (1, 16), 1.51x
-// (2, 8), 1.43x (2, 16), 1.14x (4, 8); (1, 32) 0.95x and every shape whose stream spans several
-// lanes (0.69-0.93x) stay on the materialised path.
+// the projection GEMM plus the replay (built for its one stage map) at B256 T512 C1536: 1.40x
+// (1, 8), 1.56x (2, 8), 1.13x (2, 16), 1.13x (4, 8); (1, 16) 0.91x, (1, 32) and every shape whose
+// stream spans several lanes stay on the materialised path.
 __host__ __device__ constexpr bool control_serves(int K, int M) {
-    return (K == 1 && (M == 8 || M == 16)) || (K == 2 && (M == 8 || M == 16)) || (K == 4 && M == 8);
+    return (K == 1 && M == 8) || (K == 2 && (M == 8 || M == 16)) || (K == 4 && M == 8);
 }
 
 template <int K, int M>
@@ -319,7 +319,6 @@ bool lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype)
 
 int lattice_control_launch(const LatticeControlArgs &a, hipStream_t stream) {
     if (a.K == 1 && a.M == 8) return launch_km<1, 8>(a, stream);
-    if (a.K == 1 && a.M == 16) return launch_km<1, 16>(a, stream);
     if (a.K == 2 && a.M == 8) return launch_km<2, 8>(a, stream);
     if (a.K == 2 && a.M == 16) return launch_km<2, 16>(a, stream);
     if (a.K == 4 && a.M == 8) return launch_km<4, 8>(a, stream);

@@ -119,6 +119,25 @@ def test_every_arch(torch_mod, plugin, arch):
     _assert(final, want_state, "float32", f"{arch} state")
 
 
+@pytest.mark.parametrize("order,memory,chunk", [(2, 64, 32), (2, 16, 48), (4, 32, 48)],
+                         ids=["k2m64_mfma_summary", "k2m16", "k4m32"])
+@pytest.mark.parametrize("arch", list(L.ARCH_STAGE))
+def test_every_arch_bf16_per_map_kernels(torch_mod, plugin, arch, order, memory, chunk):
+    """bf16 at the mixer's shapes runs summary and replay kernels built for the one stage map of
+    the call: every map, through the chunked path (summary, combine, replay), with a mask and a
+    carried-in state, against the fp32 oracle on the bf16-rounded inputs."""
+    rng = np.random.default_rng(60 + order + memory)
+    values = L.random_inputs(rng, 2, 100, 40, order, memory, scale=(0.5, 1.2, 0.5, 0.8, 0.5, 0.5, 1.0),
+                             beta_bias=0.3)
+    values[1][0, :4] *= 8.0                     # |alpha| > 1: the reciprocal branches
+    state = (rng.standard_normal((2, order, 40, memory)) * 0.1).astype(np.float32)
+    valid = rng.random((2, 100)) > 0.15
+    y, final = _run(plugin, torch_mod, values, valid, state, arch, "bfloat16", chunk=chunk)
+    want_y, want_state = _oracle(values, valid, state, arch, "bfloat16", torch_mod)
+    _assert(y, want_y, "bfloat16", f"{arch} output")
+    assert max_abs(final, want_state) <= 1e-4, f"{arch} state: {max_abs(final, want_state):.3e}"
+
+
 @pytest.mark.parametrize("chunk", [1, 5, 16, 17, 64, None, 1000])
 def test_chunking_is_invisible(torch_mod, plugin, chunk):
     rng = np.random.default_rng(11)
