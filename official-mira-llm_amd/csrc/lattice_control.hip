@@ -24,7 +24,7 @@
 //          the double-buffered staging area;                                   barrier
 // and the outputs of tile n leave at the start of tile n + 1. Global loads run two tiles ahead
 // into two register sets that alternate by tile parity, so a tile never waits for HBM. About
-// 35 KB of LDS and 168 VGPRs a block: three waves per SIMD. The 16-sequence tile measured 20 %
+// 35 KB of LDS and at most 168 VGPRs a block: three waves per SIMD. The 16-sequence tile measured 20 %
 // faster than 8 sequences x 2 tokens (2 blocks per CU), and forcing four waves per SIMD spilled
 // and ran 29 % slower.
 #include "lattice_common.hpp"
@@ -75,8 +75,10 @@ constexpr size_t weight_bytes(int R) { return (size_t)Shape<K, M>::NCOL * (R + 8
 
 __device__ __forceinline__ float bf16_value(uint32_t h) { return __uint_as_float((h & 0xffffu) << 16); }
 
+// at least three waves per SIMD: (K, d_m) = (4, 8) would otherwise take 172 VGPRs and two
 template <int K, int M>
-__global__ __launch_bounds__(THREADS) void lattice_control_kernel(LatticeControlArgs a) {
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(3)))
+void lattice_control_kernel(LatticeControlArgs a) {
     using S = Shape<K, M>;
     constexpr int L = S::L, TT = S::TT, SB = S::SB, G = S::G, MV = S::MV, COLS = S::COLS;
     constexpr int NCOL = S::NCOL, NC = S::NC, NW = S::NW, NR = S::NR, NX = S::NX;
