@@ -83,7 +83,7 @@ __device__ __forceinline__ void stage_coefficient_tile(const LatticeArgs &a, int
 // ---------------------------------------------------------------------------------------------
 // summary: Phi and carry of every chunk but the last, from a zero state
 // ---------------------------------------------------------------------------------------------
-template <typename IO, int K, int M>
+template <typename IO, int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
     constexpr int L = lanes_for(K, M);
     constexpr int G = BLOCK / L;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary(LatticeArgs a) {
         __syncthreads();
         for (int i = threadIdx.x; i < n * M; i += BLOCK)
             s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
-        stage_coefficient_tile<IO, K, false>(a, b, tile, n, group * G, G, s_coef, s_valid);
+        stage_coefficient_tile<IO, K, false, MODE>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
         if (!active) continue;
         for (int tt = 0; tt < n; ++tt) {
@@ -697,7 +697,7 @@ int launch_chunked(LatticeArgs &a, hipStream_t stream) {
         }
         if (!summarised) {
             const long long blocks = (long long)a.B * (a.chunks - 1) * groups;
-            hipLaunchKernelGGL((lattice_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+            hipLaunchKernelGGL((lattice_summary<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0, stream, a);
             if (int rc = check_launch("lattice_summary")) return rc;
         }
         const long long threads = (long long)a.B * a.C * M;
@@ -712,7 +712,7 @@ int launch_chunked(LatticeArgs &a, hipStream_t stream) {
 
 // bf16 at the mixer's shapes runs summary and replay kernels built for their one stage map: the
 // fifteen maps and the branches between them in one kernel cost 9-30 % (replay at K = 2, d_m = 64
-// and 16) and 10 % (summary) against kernels that carry one map.
+// and 16) and 10 % (matrix-core summary) against kernels that carry one map.
 __host__ __device__ constexpr bool fixed_stage_map(int K, int M) {
     return (K == 1 || K == 2 || K == 4) && (M == 16 || M == 32 || M == 64 || M == 128);
 }
