@@ -342,9 +342,12 @@ def _control_scan(x, control, weight, bias, spans, gamma, memory_write, valid, s
 
     row, gamma_row = plan
     batch, tokens, channels = x.shape
-    (alpha_lo, alpha_hi), (beta_lo, _), (rho_lo, _), (read_lo, read_hi) = spans
-    if alpha_hi - alpha_lo != channels * order:
-        raise ValueError("mira-dsp: the alpha span must hold channels x order rows")
+    (alpha_lo, alpha_hi), (beta_lo, beta_hi), (rho_lo, rho_hi), (read_lo, read_hi) = spans
+    if (alpha_hi - alpha_lo != channels * order or beta_hi - beta_lo != channels * order
+            or rho_hi - rho_lo != channels * (order + 1)
+            or read_hi - read_lo != (order + 1) * memory):
+        raise ValueError("mira-dsp: the coefficient spans must hold C K, C K, C (K+1) and "
+                         "(K+1) d_m rows")
     if valid is not None:
         if valid.shape != (batch, tokens) or valid.device != x.device or valid.dtype != torch.bool:
             raise ValueError("mira-dsp mask must be a boolean [batch, tokens] CUDA tensor")

@@ -194,6 +194,10 @@ def test_errors(torch_mod, plugin):
             plugin.matrix_lattice_iir_control(*args, state=torch.zeros(2, 2, 32, 16, device="cuda"))
         with pytest.raises(ValueError):
             plugin.matrix_lattice_iir_control(*args, valid=torch.ones(2, 3, device="cuda"))
+        (a0, a1), (b0, b1), (r0, r1), (n0, n1) = v["spans"]
+        short_rho = ((a0, a1), (b0, b1), (r0, r1 - 1), (n0, n1))
+        with pytest.raises(ValueError):
+            plugin.matrix_lattice_iir_control(*args[:4], short_rho, *args[5:])
 
 
 def test_mixer_eval_forward_takes_the_control_scan(torch_mod, plugin):
