@@ -23,8 +23,10 @@
 //          rows, s and nu rows, x, gamma, valid flags) go from registers into the other half of
 //          the double-buffered staging area;                                   barrier
 // and the outputs of tile n leave at the start of tile n + 1. Global loads run two tiles ahead
-// into two register sets that alternate by tile parity, so a tile never waits for HBM. About
-// 35 KB of LDS and at most 168 VGPRs a block: three waves per SIMD. The 16-sequence tile measured 20 %
+// into two register sets that alternate by tile parity, so a tile never waits for HBM. One kernel
+// per stage map (as the reference builds its fused scans): 7-14 % faster than one kernel that
+// reads the map at run time. About 35 KB of LDS and at most 168 VGPRs a block: three waves per
+// SIMD. The 16-sequence tile measured 20 %
 // faster than 8 sequences x 2 tokens (2 blocks per CU), and forcing four waves per SIMD spilled
 // and ran 29 % slower.
 #include "lattice_common.hpp"
@@ -45,9 +47,10 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // The (K, d_m) served: one lane holds a whole stream (K d_m <= 32) and the scan's work per
 // (token, channel) is small next to the 3K + 1 coefficients it saves reading. Measured against
-// the projection GEMM plus the replay (built for its one stage map) at B256 T512 C1536: 1.40x
-// (1, 8), 1.56x (2, 8), 1.13x (2, 16), 1.13x (4, 8); (1, 16) 0.91x, (1, 32) and every shape whose
-// stream spans several lanes stay on the materialised path.
+// the projection GEMM plus the replay (both built for the call's one stage map) at B256 T512
+// C1536: 1.40x (1, 8), 1.74x (2, 8), 1.21x (2, 16), 1.30x (4, 8); (1, 16) 0.91x (before this
+// kernel was built per map), (1, 32) and every shape whose stream spans several lanes stay on the
+// materialised path.
 __host__ __device__ constexpr bool control_serves(int K, int M) {
     return (K == 1 && M == 8) || (K == 2 && (M == 8 || M == 16)) || (K == 4 && M == 8);
 }
@@ -76,7 +79,7 @@ constexpr size_t weight_bytes(int R) { return (size_t)Shape<K, M>::NCOL * (R + 8
 __device__ __forceinline__ float bf16_value(uint32_t h) { return __uint_as_float((h & 0xffffu) << 16); }
 
 // at least three waves per SIMD: (K, d_m) = (4, 8) would otherwise take 172 VGPRs and two
-template <int K, int M>
+template <int K, int M, int MODE>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(3)))
 void lattice_control_kernel(LatticeControlArgs a) {
     using S = Shape<K, M>;
@@ -220,7 +223,8 @@ void lattice_control_kernel(LatticeControlArgs a) {
             V[k][v] = active && a.state_in
                           ? a.state_in[(((long long)b * K + k) * a.C + c) * M + slot<M, L>(lane, v)]
                           : 0.0f;
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    const int mode = MODE ? MODE : a.mode;             // MODE: the stage map compiled in
+    const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
 
     // tile n: store n - 1, form, scan n, stage n + 1 from `use`, load n + 2 into `fill`
     auto iteration = [&](int n, Pre &fill, const Pre &use) {
@@ -297,17 +301,40 @@ void lattice_control_kernel(LatticeControlArgs a) {
     }
 }
 
-template <int K, int M>
+template <int K, int M, int MODE>
 int launch_km(const LatticeControlArgs &a, hipStream_t stream) {
     using S = Shape<K, M>;
     const size_t dynamic = weight_bytes<K, M>(a.R);
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&lattice_control_kernel<K, M>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&lattice_control_kernel<K, M, MODE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)dynamic) != hipSuccess)
         return fail(MIRA_ERR_HIP, "lattice_control_kernel: cannot raise the dynamic LDS limit");
     const long long blocks = (long long)((a.B + S::SB - 1) / S::SB) * ((a.C + S::G - 1) / S::G);
-    hipLaunchKernelGGL((lattice_control_kernel<K, M>), dim3(blocks), dim3(THREADS), dynamic,
+    hipLaunchKernelGGL((lattice_control_kernel<K, M, MODE>), dim3(blocks), dim3(THREADS), dynamic,
                        stream, a);
     return check_launch("lattice_control_kernel");
+}
+
+// one kernel per stage map
+template <int K, int M>
+int launch_mode(const LatticeControlArgs &a, hipStream_t stream) {
+    switch (a.mode) {
+        case 3: return launch_km<K, M, 3>(a, stream);
+        case 6: return launch_km<K, M, 6>(a, stream);
+        case 7: return launch_km<K, M, 7>(a, stream);
+        case 8: return launch_km<K, M, 8>(a, stream);
+        case 9: return launch_km<K, M, 9>(a, stream);
+        case 10: return launch_km<K, M, 10>(a, stream);
+        case 11: return launch_km<K, M, 11>(a, stream);
+        case 12: return launch_km<K, M, 12>(a, stream);
+        case 13: return launch_km<K, M, 13>(a, stream);
+        case 14: return launch_km<K, M, 14>(a, stream);
+        case 15: return launch_km<K, M, 15>(a, stream);
+        case 16: return launch_km<K, M, 16>(a, stream);
+        case 17: return launch_km<K, M, 17>(a, stream);
+        case 18: return launch_km<K, M, 18>(a, stream);
+        case 19: return launch_km<K, M, 19>(a, stream);
+    }
+    return launch_km<K, M, 0>(a, stream);
 }
 
 }  // namespace
@@ -320,10 +347,10 @@ bool lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype)
 }
 
 int lattice_control_launch(const LatticeControlArgs &a, hipStream_t stream) {
-    if (a.K == 1 && a.M == 8) return launch_km<1, 8>(a, stream);
-    if (a.K == 2 && a.M == 8) return launch_km<2, 8>(a, stream);
-    if (a.K == 2 && a.M == 16) return launch_km<2, 16>(a, stream);
-    if (a.K == 4 && a.M == 8) return launch_km<4, 8>(a, stream);
+    if (a.K == 1 && a.M == 8) return launch_mode<1, 8>(a, stream);
+    if (a.K == 2 && a.M == 8) return launch_mode<2, 8>(a, stream);
+    if (a.K == 2 && a.M == 16) return launch_mode<2, 16>(a, stream);
+    if (a.K == 4 && a.M == 8) return launch_mode<4, 8>(a, stream);
     return fail(MIRA_DECLINE, "lattice control: unsupported (K, d_m)");
 }
 
