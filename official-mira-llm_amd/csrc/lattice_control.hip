@@ -48,7 +48,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 // The (K, d_m) served: one lane holds a whole stream (K d_m <= 32) and the scan's work per
 // (token, channel) is small next to the 3K + 1 coefficients it saves reading. Measured against
 // the projection GEMM plus the replay (both built for the call's one stage map) at B256 T512
-// C1536: 1.40x (1, 8), 1.74x (2, 8), 1.21x (2, 16), 1.30x (4, 8); (1, 16) 0.91x (before this
+// C1536: 1.41x (1, 8), 1.85x (2, 8), 1.27x (2, 16), 1.33x (4, 8); (1, 16) 0.91x (before this
 // kernel was built per map), (1, 32) and every shape whose stream spans several lanes stay on the
 // materialised path.
 __host__ __device__ constexpr bool control_serves(int K, int M) {
@@ -149,35 +149,56 @@ void lattice_control_kernel(LatticeControlArgs a) {
         uint32_t valid;
     };
     const int cpieces = R / 8;                                 // 16-byte pieces of a control row
-    auto row_of = [&](int n, int r, long long &index) {
-        const int rb = b0 + r % SB, rt = n * TT + r / SB;
-        index = (long long)rb * a.T + rt;
-        return rb < a.B && rt < a.T;
+    // Every thread loads the same rows of every tile, TT tokens further on: a load slot keeps its
+    // element offset at tile 0 and how many tokens its row has left (0 past the batch), so a tile
+    // costs one uniform product and one add per slot instead of the whole row arithmetic.
+    struct Slot { long long base; int room; };
+    auto slot_of = [&](int r, long long stride, long long column) {
+        const int rb = b0 + r % SB, tok = r / SB;
+        return Slot{((long long)rb * a.T + tok) * stride + column, rb < a.B ? a.T - tok : 0};
     };
+    const Slot none{0, 0};
+    const Slot s_ctl_slot = tid < ROWS * cpieces ? slot_of(tid / cpieces, R, 8 * (tid % cpieces)) : none;
+    Slot s_w_slot[NW], s_r_slot[NR], s_x_slot[NX];
+    long long g_base[NX], o_base[NX];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int i = tid + j * THREADS;
+        s_w_slot[j] = i < ROWS * M / 2 ? slot_of(i / (M / 2), M / 2, i % (M / 2)) : none;
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        const int i = tid + j * THREADS;
+        s_r_slot[j] = i < ROWS * RW / 2 ? slot_of(i / (RW / 2), a.read_row / 2, i % (RW / 2)) : none;
+    }
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+        const int i = tid + j * THREADS, r = i / G, ch = i % G;
+        const bool on = i < ROWS * G && c0 + ch < a.C;
+        s_x_slot[j] = on ? slot_of(r, a.x_row, c0 + ch) : none;
+        g_base[j] = slot_of(r, a.gamma_row, c0 + ch).base;
+        o_base[j] = slot_of(r, a.C, c0 + ch).base;
+    }
+    const Slot s_v_slot = tid < ROWS ? slot_of(tid, 1, 0) : none;
     auto fetch = [&](Pre &p, int n) {
-        long long index;
+        const int t0 = n * TT;
         p.ctl = u32x4{0u, 0u, 0u, 0u};
-        if (tid < ROWS * cpieces && row_of(n, tid / cpieces, index))
-            p.ctl = *reinterpret_cast<const u32x4 *>(control + index * R + 8 * (tid % cpieces));
+        if (t0 < s_ctl_slot.room)
+            p.ctl = *reinterpret_cast<const u32x4 *>(control + s_ctl_slot.base + (long long)t0 * R);
 #pragma unroll
-        for (int j = 0; j < NW; ++j) {
-            const int i = tid + j * THREADS, r = i / (M / 2), e = i % (M / 2);
-            p.w[j] = i < ROWS * M / 2 && row_of(n, r, index) ? write2[index * (M / 2) + e] : 0u;
-        }
+        for (int j = 0; j < NW; ++j)
+            p.w[j] = t0 < s_w_slot[j].room ? write2[s_w_slot[j].base + (long long)t0 * (M / 2)] : 0u;
 #pragma unroll
-        for (int j = 0; j < NR; ++j) {
-            const int i = tid + j * THREADS, r = i / (RW / 2), e = i % (RW / 2);
-            p.r[j] = i < ROWS * RW / 2 && row_of(n, r, index) ? read2[index * (a.read_row / 2) + e] : 0u;
-        }
+        for (int j = 0; j < NR; ++j)
+            p.r[j] = t0 < s_r_slot[j].room
+                         ? read2[s_r_slot[j].base + (long long)t0 * (a.read_row / 2)] : 0u;
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
-            const int i = tid + j * THREADS, r = i / G, ch = i % G;
-            const bool on = i < ROWS * G && c0 + ch < a.C && row_of(n, r, index);
-            p.x[j] = on ? xs[index * a.x_row + c0 + ch] : 0u;
-            p.g[j] = on ? gs[index * a.gamma_row + c0 + ch] : 0u;
+            const bool on = t0 < s_x_slot[j].room;
+            p.x[j] = on ? xs[s_x_slot[j].base + (long long)t0 * a.x_row] : 0u;
+            p.g[j] = on ? gs[g_base[j] + (long long)t0 * a.gamma_row] : 0u;
         }
-        p.valid = 0u;
-        if (tid < ROWS && row_of(n, tid, index)) p.valid = !a.valid || a.valid[index];
+        p.valid = t0 < s_v_slot.room ? (!a.valid || a.valid[s_v_slot.base + t0]) : 0u;
     };
     auto stage = [&](const Pre &p, int buf) {
         if (tid < ROWS * cpieces)
@@ -207,11 +228,12 @@ void lattice_control_kernel(LatticeControlArgs a) {
         if (tid < ROWS) s_valid[buf][tid] = (unsigned char)p.valid;
     };
     auto store = [&](int n) {
-        const int buf = n & 1;
-        for (int i = tid; i < ROWS * G; i += THREADS) {
-            const int r = i / G, ch = i % G;
-            long long index;
-            if (c0 + ch < a.C && row_of(n, r, index)) out[index * a.C + c0 + ch] = s_out[buf][r][ch];
+        const int buf = n & 1, t0 = n * TT;
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            const int i = tid + j * THREADS;
+            if (t0 < s_x_slot[j].room)
+                out[o_base[j] + (long long)t0 * a.C] = s_out[buf][i / G][i % G];
         }
     };
 
