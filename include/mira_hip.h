@@ -96,7 +96,7 @@ int mira_lattice_step(const void *x, int64_t x_row, const void *alpha, int64_t a
  * and bias [weight_rows] (or NULL). control [B,T,R] contiguous; the other arguments are
  * mira_lattice_forward's, bf16 only; memory_read is the caller's projection of the control.
  * state_in and state_out may be the same buffer. mira_lattice_control_serves says whether a call
- * is served: bf16; (K, d_m) in {(1,8), (2,8), (2,16), (4,8)} (the reference serves (2,16)),
+ * is served: bf16; (K, d_m) in {(1,8), (1,16), (2,8), (2,16), (4,8)} (the reference serves (2,16)),
  * where it is faster than the projection GEMM plus mira_lattice_forward; R in {16,32,48,64}; and
  * one token chunk covers the call, mira_lattice_plan_chunk(B,T,C,K,M) >= T (the reference's fused
  * plan asks for one inference chunk, mira.py:1642-1672). A call it does not serve returns

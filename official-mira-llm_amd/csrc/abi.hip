@@ -138,8 +138,8 @@ int mira_lattice_control_forward(const void *x, int64_t x_row, const void *contr
         return fail(MIRA_ERR_ARG, "mira: requires nonempty batch, token, channel and control axes");
     if (!arch_valid(arch_mode)) return fail(MIRA_ERR_ARG, "mira: unknown arch mode");
     if (!lattice_control_serves(B, T, C, K, M, R, dtype))
-        return fail(MIRA_DECLINE, "mira: the control scan serves bf16, (K, d_m) in {(1,8), (2,8), "
-                                  "(2,16), (4,8)}, d_r in {16,32,48,64} and calls one token "
+        return fail(MIRA_DECLINE, "mira: the control scan serves bf16, (K, d_m) in {(1,8), (1,16), "
+                                  "(2,8), (2,16), (4,8)}, d_r in {16,32,48,64} and calls one token "
                                   "chunk covers");
     if (!x || !control || !weight || !gamma || !memory_write || !memory_read || !out)
         return fail(MIRA_ERR_ARG, "mira: a required tensor is null");

@@ -44,15 +44,16 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // The (K, d_m) served: one lane holds a whole stream (K d_m <= 32) and the scan's work per
 // (token, channel) is small next to the 3K + 1 coefficients it saves reading. Measured against
 // the projection GEMM plus the replay (both built for the call's one stage map) at B256 T512
-// C1536: 1.41x (1, 8), 1.85x (2, 8), 1.27x (2, 16), 1.33x (4, 8); (1, 16) 0.91x (before this
-// kernel was built per map), (1, 32) and every shape whose stream spans several lanes stay on the
-// materialised path.
+// C1536: 1.64x (1, 8), 1.07-1.16x (1, 16), 2.15x (2, 8), 1.38x (2, 16), 1.59x (4, 8); (1, 32)
+// 0.92x and every shape whose stream spans several lanes stay on the materialised path.
 __host__ __device__ constexpr bool control_serves(int K, int M) {
-    return (K == 1 && M == 8) || (K == 2 && (M == 8 || M == 16)) || (K == 4 && M == 8);
+    return (K == 1 && (M == 8 || M == 16)) || (K == 2 && (M == 8 || M == 16)) || (K == 4 && M == 8);
 }
 
 template <int K, int M>
@@ -77,6 +78,11 @@ template <int K, int M>
 constexpr size_t weight_bytes(int R) { return (size_t)Shape<K, M>::NCOL * (R + 8) * 2; }
 
 __device__ __forceinline__ float bf16_value(uint32_t h) { return __uint_as_float((h & 0xffffu) << 16); }
+
+// two floats rounded to bf16 (nearest even) in one conversion: lo in bits 0-15, hi in 16-31
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
 
 // at least three waves per SIMD: (K, d_m) = (4, 8) would otherwise take 172 VGPRs and two
 template <int K, int M, int MODE>
@@ -265,8 +271,13 @@ void lattice_control_kernel(LatticeControlArgs a) {
                     *reinterpret_cast<const s16x4 *>(wrow + k0), acc, 0, 0, 0);
             const int col = 16 * ct + (wl & 15);
             const float bcol = s_bias[col];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s_raw[4 * (wl >> 4) + e][col] = bf16_bits(acc[e] + bcol);
+            const uint32_t p01 = bf16_pair(acc[0] + bcol, acc[1] + bcol);
+            const uint32_t p23 = bf16_pair(acc[2] + bcol, acc[3] + bcol);
+            const int row = 4 * (wl >> 4);
+            s_raw[row][col] = (uint16_t)p01;
+            s_raw[row + 1][col] = (uint16_t)(p01 >> 16);
+            s_raw[row + 2][col] = (uint16_t)p23;
+            s_raw[row + 3][col] = (uint16_t)(p23 >> 16);
         }
         __syncthreads();
         // ---- scan: every stream forms its own coefficients from the raw columns, then steps;
@@ -297,7 +308,7 @@ void lattice_control_kernel(LatticeControlArgs a) {
                 if (s_valid[buf][r])
                     y = lattice_token<K, M, L>(V, [&](int q) { return mine[tt][q]; },
                                                s_write[buf][r], s_read[buf][r], lane);
-                s_out[buf][r][cl] = bf16_bits(y);
+                s_out[buf][r][cl] = (uint16_t)bf16_pair(y, 0.0f);
             }
         }
         if (n + 1 < tiles) stage(use, buf ^ 1);
@@ -370,6 +381,7 @@ bool lattice_control_serves(int B, int T, int C, int K, int M, int R, int dtype)
 
 int lattice_control_launch(const LatticeControlArgs &a, hipStream_t stream) {
     if (a.K == 1 && a.M == 8) return launch_mode<1, 8>(a, stream);
+    if (a.K == 1 && a.M == 16) return launch_mode<1, 16>(a, stream);
     if (a.K == 2 && a.M == 8) return launch_mode<2, 8>(a, stream);
     if (a.K == 2 && a.M == 16) return launch_mode<2, 16>(a, stream);
     if (a.K == 4 && a.M == 8) return launch_mode<4, 8>(a, stream);

@@ -96,7 +96,7 @@ def test_control_scan_plan_and_errors(lib):
     is the faster path, d_r in {16, 32, 48, 64}, one token chunk; anything else declines before
     any HIP call, and coefficient rows outside the weight are a bad argument."""
     bf16, f32 = 1, 0
-    served = {(1, 8), (2, 8), (2, 16), (4, 8)}
+    served = {(1, 8), (1, 16), (2, 8), (2, 16), (4, 8)}
     for K in (1, 2, 4, 8):
         for M in (8, 16, 32, 64):
             want = int((K, M) in served)

@@ -141,14 +141,14 @@ def test_every_arch(torch_mod, plugin, number, arch):
           number % 2 == 1, number % 3 == 0, arch)
 
 
-@pytest.mark.parametrize("order,memory", [(1, 8), (2, 8), (4, 8)])
+@pytest.mark.parametrize("order,memory", [(1, 8), (1, 16), (2, 8), (4, 8)])
 def test_orders_and_memories(torch_mod, plugin, order, memory):
     """The other served shapes beside the reference's one (K=2, d_m=16)."""
     _case(plugin, torch_mod, 9, 11, 48, 32, True, True, "cauchy_x_hyperbolic", order=order,
           memory=memory)
 
 
-@pytest.mark.parametrize("order,memory", [(1, 16), (1, 32), (2, 32), (2, 64), (4, 16)])
+@pytest.mark.parametrize("order,memory", [(1, 32), (2, 32), (2, 64), (4, 16)])
 def test_unserved_shapes_fall_back(torch_mod, plugin, order, memory):
     """(K, d_m) where the materialised path is the faster one: bit for bit that path."""
     _case(plugin, torch_mod, 9, 11, 48, 32, True, True, "cauchy_x_hyperbolic", order=order,
