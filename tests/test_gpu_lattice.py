@@ -138,6 +138,21 @@ def test_every_arch_bf16_per_map_kernels(torch_mod, plugin, arch, order, memory,
     assert max_abs(final, want_state) <= 1e-4, f"{arch} state: {max_abs(final, want_state):.3e}"
 
 
+@pytest.mark.parametrize("order,memory", [(1, 16), (1, 128), (2, 32), (2, 128), (4, 16), (4, 128)])
+@pytest.mark.parametrize("arch", ["cauchy_x_mobius", "hill_x_identity"])
+def test_per_map_kernels_other_shapes(torch_mod, plugin, arch, order, memory):
+    """The rest of the (K, d_m) built per stage map in bf16, chunked (48-token chunks: the matrix
+    summary at d_m >= 32, the per-slot one below), with a mask and a carried-in state."""
+    rng = np.random.default_rng(90 + order + memory)
+    values = L.random_inputs(rng, 2, 100, 24, order, memory)
+    state = (rng.standard_normal((2, order, 24, memory)) * 0.1).astype(np.float32)
+    valid = rng.random((2, 100)) > 0.15
+    y, final = _run(plugin, torch_mod, values, valid, state, arch, "bfloat16", chunk=48)
+    want_y, want_state = _oracle(values, valid, state, arch, "bfloat16", torch_mod)
+    _assert(y, want_y, "bfloat16", f"{arch} K{order} d_m{memory} output")
+    assert max_abs(final, want_state) <= 1e-4, f"state: {max_abs(final, want_state):.3e}"
+
+
 @pytest.mark.parametrize("chunk", [1, 5, 16, 17, 64, None, 1000])
 def test_chunking_is_invisible(torch_mod, plugin, chunk):
     rng = np.random.default_rng(11)
