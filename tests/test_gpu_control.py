@@ -177,6 +177,56 @@ def test_fully_masked_rows_keep_the_state(torch_mod, plugin):
     assert torch.equal(final[2], v["state"][2])
 
 
+def test_without_bias_and_with_a_strided_control(torch_mod, plugin):
+    """coefficient_projection without a bias, and a control that is a column slice of a wider
+    tensor (the wrapper makes it contiguous): still the fused path, still the materialised result."""
+    import torch.nn.functional as F
+
+    torch = torch_mod
+    B, T, C, K, M, R = 20, 6, 64, 2, 16, 32
+    v = _inputs(torch, B, T, C, R, K, M, True, True, 21)
+    wide = torch.randn(B, T, R + 16, device="cuda").to(torch.bfloat16)
+    wide[..., 8:8 + R] = v["control"]
+    control = wide[..., 8:8 + R]
+    assert not control.is_contiguous()
+    before = plugin.usage()["control"]
+    with torch.no_grad():
+        got, got_final = plugin.matrix_lattice_iir_control(
+            v["signal"], control, v["weight"], None, v["spans"], v["gamma"], v["write"],
+            valid=v["valid"], state=v["state"], return_state=True)
+        assert plugin.usage()["control"] == before + 1
+        coefficients = F.linear(v["control"], v["weight"])
+        alpha, beta, rho, read = coefficients.split(tuple(hi - lo for lo, hi in v["spans"]), dim=-1)
+        want, want_final = plugin.matrix_lattice_iir(
+            v["signal"], alpha.view(B, T, C, K), rho.view(B, T, C, K + 1), v["gamma"], v["write"],
+            read.view(B, T, K + 1, M), raw_beta=beta.view(B, T, C, K), valid=v["valid"],
+            state=v["state"], return_state=True)
+    torch.cuda.synchronize()
+    assert float((got != want).float().mean()) <= 0.02
+    assert scaled(to_numpy(got), to_numpy(want)) <= HALF_SCALED
+    assert scaled(to_numpy(got_final), to_numpy(want_final)) <= HALF_SCALED
+
+
+@pytest.mark.parametrize("what", ["float32", "weight_columns_strided"])
+def test_unserved_layouts_fall_back(torch_mod, plugin, what):
+    """A float32 call, or a weight whose rows are not contiguous: the materialised path."""
+    torch = torch_mod
+    B, T, C, K, M, R = 4, 5, 32, 2, 16, 16
+    v = _inputs(torch, B, T, C, R, K, M, False, False, 31)
+    weight = v["weight"]
+    args = [v["signal"], v["control"], weight, v["bias"], v["spans"], v["gamma"], v["write"]]
+    if what == "float32":
+        args = [t.float() if hasattr(t, "float") else t for t in args]
+    else:
+        args[2] = torch.empty(weight.shape[1], weight.shape[0], device="cuda",
+                              dtype=weight.dtype).copy_(weight.t()).t()      # column-major view
+        assert args[2].stride(1) != 1
+    before = plugin.usage()["control"]
+    with torch.no_grad():
+        got = plugin.matrix_lattice_iir_control(*args)
+    assert got is not None and plugin.usage()["control"] == before
+
+
 def test_split_sequence_falls_back_bit_for_bit(torch_mod, plugin):
     _case(plugin, torch_mod, 1, 300, 1536, 48, expect_fused=False)
 
