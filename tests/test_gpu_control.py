@@ -148,6 +148,14 @@ def test_orders_and_memories(torch_mod, plugin, order, memory):
           memory=memory)
 
 
+@pytest.mark.parametrize("order,memory", [(1, 8), (1, 16), (2, 8), (4, 8)])
+@pytest.mark.parametrize("arch", list(L.ARCH_STAGE))
+def test_every_map_at_every_served_shape(torch_mod, plugin, arch, order, memory):
+    """The kernel is built once per stage map and served shape: every one of them runs, with a
+    mask and a carried-in state, against the materialised path and the oracle."""
+    _case(plugin, torch_mod, 7, 5, 40, 16, True, True, arch, order=order, memory=memory)
+
+
 @pytest.mark.parametrize("order,memory", [(1, 32), (2, 32), (2, 64), (4, 16)])
 def test_unserved_shapes_fall_back(torch_mod, plugin, order, memory):
     """(K, d_m) where the materialised path is the faster one: bit for bit that path."""
