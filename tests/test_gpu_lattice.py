@@ -138,11 +138,11 @@ def test_every_arch_bf16_per_map_kernels(torch_mod, plugin, arch, order, memory,
     assert max_abs(final, want_state) <= 1e-4, f"{arch} state: {max_abs(final, want_state):.3e}"
 
 
-@pytest.mark.parametrize("order,memory", [(1, 16), (1, 128), (2, 32), (2, 128), (4, 16), (4, 128)])
-@pytest.mark.parametrize("arch", ["cauchy_x_mobius", "hill_x_identity"])
-def test_per_map_kernels_other_shapes(torch_mod, plugin, arch, order, memory):
-    """The rest of the (K, d_m) built per stage map in bf16, chunked (48-token chunks: the matrix
-    summary at d_m >= 32, the per-slot one below), with a mask and a carried-in state."""
+@pytest.mark.parametrize("order,memory", [(k, m) for k in (1, 2, 4) for m in (16, 32, 64, 128)])
+@pytest.mark.parametrize("arch", list(L.ARCH_STAGE))
+def test_per_map_kernels_every_shape(torch_mod, plugin, arch, order, memory):
+    """Every (K, d_m) built per stage map in bf16 under every map, chunked (48-token chunks: the
+    matrix summary at d_m >= 32, the per-slot one below), with a mask and a carried-in state."""
     rng = np.random.default_rng(90 + order + memory)
     values = L.random_inputs(rng, 2, 100, 24, order, memory)
     state = (rng.standard_normal((2, order, 24, memory)) * 0.1).astype(np.float32)
