@@ -123,9 +123,13 @@ int mira_lattice_control_forward(const void *x, int64_t x_row, const void *contr
  *   ring_in / ring_out [B,D,W-1] (dtype) or NULL: slot s holds x of the stream token t' = s
  *   (mod W-1) among the last W-1; pos = tokens the stream absorbed before this call. ring_out may
  *   equal ring_in.
- * Prefill is one pass over HBM (decoupled look-back across token tiles); its workspace
- * (mira_diag_workspace_bytes) must be zero-filled once when first allocated and then only reused
- * by calls on one stream at a time. W must be 4; D a multiple of 8 (bf16/f16) or 4 (f32). */
+ * Prefill is one pass over HBM. Where the batch has a 64-channel column for at least half the
+ * CUs (B * ceil(D/64) >= CUs/2, e.g. BASELINE cfg2) one workgroup scans each column over all T
+ * and the workspace is not touched; narrower batches split the tokens into tiles joined by a
+ * decoupled look-back, whose workspace (mira_diag_workspace_bytes) must be zero-filled once when
+ * first allocated and then only reused by calls on one stream at a time. The look-back form
+ * refuses HIP-graph capture (MIRA_ERR_ARG): its per-launch epoch would be frozen into the graph.
+ * W must be 4; D a multiple of 4. */
 size_t mira_diag_workspace_bytes(int B, int T, int D, int dtype);
 int mira_diag_conv_scan(const void *x, const void *a, const float *w, const float *bias,
                         const float *h0, const void *ring_in, void *ring_out, int64_t pos,

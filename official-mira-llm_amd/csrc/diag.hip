@@ -960,6 +960,13 @@ int scan_typed(const DiagArgs &a, void *ws, size_t bytes, hipStream_t stream) {
         hipLaunchKernelGGL((diag_column_kernel<IO, 4>), dim3(columns), dim3(COL_WAVES * 64), 0, stream, a);
         return check_launch("diag_column");
     }
+    // The look-back form tags its flags with a per-launch epoch passed as an argument, so a
+    // graph replay would reuse a captured epoch and could read a previous replay's records:
+    // refuse capture rather than risk a silently wrong prefill.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+        return fail(MIRA_ERR_ARG, "diag: the look-back prefill (batches with fewer 64-channel "
+                                  "columns than half the CUs) cannot be captured in a HIP graph");
     unsigned epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
     if (epoch == 0) epoch = (g_epoch.fetch_add(1) + 1) & 0x3fffffffu;
     // persistent workgroups: one per CU in all, spread evenly over the chains

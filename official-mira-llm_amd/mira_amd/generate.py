@@ -2,8 +2,9 @@
 (mirachat.py:753-849), batched.
 
 The prompt goes through the model in one forward that leaves every layer's lattice state in a
-PrefixCache; each new token is then one T = 1 step per layer, the state updated in place
-(mira_amd.mixer routes a cached single-token call to matrix_lattice_step). Sampling follows the
+PrefixCache; each new token is then one T = 1 step per layer, the state updated in place (the
+loop owns its cache and sets PrefixCache.in_place, so mira_amd.mixer's single-token call
+overwrites the held state through matrix_lattice_step). Sampling follows the
 reference's rule (mirachat.py:824-838): greedy at temperature <= 0, else logits / temperature,
 top-k masking, softmax, top-p truncation that always keeps the most likely token, and one draw.
 
@@ -79,6 +80,7 @@ def generate(model, prompt_ids, max_new, temperature=0.0, top_k=0, top_p=1.0, eo
         raise ValueError("generate decodes through the prefix cache, which needs model.eval()")
     batch = prompt_ids.shape[0]
     cache = PrefixCache(len(model.blocks))
+    cache.in_place = True                # this loop owns the cache and keeps no earlier states
     logits = model(prompt_ids, cache=cache).logits[:, -1]
     step = None
     out = []

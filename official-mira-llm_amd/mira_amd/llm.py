@@ -43,6 +43,9 @@ class MiraLLM(nn.Module):
                         memory_dimension=int(memory_dimension),
                         ffn_hidden=int(ffn_hidden or 4 * n_embd), arch=arch)
         self.tok = nn.Embedding(vocab_size, n_embd)
+        # the reference's masked-token embedding (model/mira_llm.py:136): kept so a reference
+        # state_dict loads as is; masked-token substitution itself is not built here
+        self.mask_embed = nn.Parameter(torch.zeros(n_embd))
         self.drop = nn.Dropout(dropout)
         self.blocks = nn.ModuleList([
             MiraBlock(n_embd, dropout=dropout, lattice_order=self.cfg["lattice_order"],
@@ -69,6 +72,13 @@ class MiraLLM(nn.Module):
                 nn.init.zeros_(m.bias)
         elif isinstance(m, nn.Embedding):
             nn.init.normal_(m.weight, mean=0.0, std=0.02)
+
+    def reset_states(self, lattice_states=None):
+        """Empty every slot of a PrefixCache's state list (model/mira_llm.py:311-315): the next
+        forward starts each layer from zeros."""
+        if lattice_states is not None:
+            for layer in range(len(lattice_states)):
+                lattice_states[layer] = None
 
     def hidden_states(self, input_ids, attention_mask=None, cache=None):
         """The trunk's output (B, T, n_embd) before the head."""

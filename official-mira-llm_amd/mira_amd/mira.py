@@ -298,6 +298,11 @@ def _control_plan(x, control, weight, bias, gamma, memory_write, order, memory):
     row, gamma_row = _row_stride(x, tokens), _row_stride(gamma, tokens)
     if row is None or gamma_row is None or row < channels or gamma_row < channels:
         return None
+    # the kernel reads control rows as 16-byte pieces and weight rows as 8-byte pieces
+    # (mira_lattice_control_forward declines otherwise); such a call takes GEMM + scan instead
+    if (control.contiguous().data_ptr() % 16 or weight.data_ptr() % 8
+            or weight.stride(0) % 4):
+        return None
     return row, gamma_row
 
 

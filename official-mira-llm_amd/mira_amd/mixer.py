@@ -21,6 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import mira as plugin
+from . import prefix_cache
 
 ARCHES = tuple(plugin.ARCH_STAGE)
 
@@ -32,6 +33,32 @@ def _declined(signal, order, memory_dimension):
             f"d_m={memory_dimension} K={order} dtype={signal.dtype}: {detail}. "
             f"MIRA does not fall back to a PyTorch scan -- build the library with "
             f"python official-mira-llm_amd/build.py")
+
+
+def _plain_linear(module):
+    return (type(module) is nn.Linear and not module._forward_pre_hooks
+            and not module._forward_hooks and "forward" not in module.__dict__)
+
+
+def _packing_signature(normalized_x, projections):
+    """The key of the packed input-projection weight, or None when packing would bypass
+    something a module call does (a tensor subclass, a global or module hook, a subclassed or
+    patched Linear, a parameter that is not a plain nn.Parameter)."""
+    from torch.nn.modules import module as module_globals
+
+    if type(normalized_x) is not torch.Tensor:
+        return None
+    if module_globals._global_forward_pre_hooks or module_globals._global_forward_hooks:
+        return None
+    if not all(_plain_linear(p) for p in projections):
+        return None
+    parameters = [t for p in projections for t in (p.weight, p.bias) if t is not None]
+    if not all(type(t) is nn.Parameter for t in parameters):
+        return None
+    stream = (torch.cuda.current_stream(normalized_x.device).cuda_stream
+              if normalized_x.is_cuda else None)
+    return (tuple((id(t), t.data_ptr(), t._version, t.dtype, t.device, tuple(t.shape),
+                   tuple(t.stride())) for t in parameters), stream)
 
 
 class MiraMixer(nn.Module):
@@ -85,21 +112,25 @@ class MiraMixer(nn.Module):
 
     def project_recurrence_inputs(self, normalized_x, coefficients=True):
         """(input projection, coefficient projection, gamma) of the normalised input, or with
-        coefficients=False (input projection, control, gamma) (model/mira_mixer.py:657-712). In
-        inference the three projections run as one GEMM on a packed weight kept between calls and
-        rebuilt when any of the parameters changes (its storage, version, dtype or shape), so a
-        decode step reads the weights once instead of copying them first; with gradients they
-        run as three projections."""
+        coefficients=False (input projection, control, gamma) (model/mira_mixer.py:657-712).
+
+        In inference the three input projections run as one GEMM on a packed weight kept
+        between calls, so a decode step reads the weights once instead of concatenating them
+        every time. That shortcut calls no module, so it is taken only when calling the modules
+        would do exactly the same: a plain torch.Tensor input, no global module hooks, and three
+        plain nn.Linear projections with no hooks, no replaced forward and plain nn.Parameter
+        weights. The packed weight is rebuilt whenever any parameter's identity, storage,
+        version, dtype, device, shape or strides change, or the call runs on another stream.
+        Otherwise (and with gradients) the three modules are called."""
         projections = (self.input_projection, self.to_gate, self.to_control)
         finish = self.coefficient_projection if coefficients else (lambda control: control)
-        if self.training or torch.is_grad_enabled():
+        signature = None
+        if not self.training and not torch.is_grad_enabled():
+            signature = _packing_signature(normalized_x, projections)
+        if signature is None:
             control = F.silu(self.to_control(normalized_x))
             return (self.input_projection(normalized_x), finish(control),
                     self.to_gate(normalized_x))
-        parameters = [p.weight for p in projections] + [p.bias for p in projections
-                                                        if p.bias is not None]
-        signature = tuple((id(p), p.data_ptr(), p._version, p.dtype, p.device, tuple(p.shape))
-                          for p in parameters)
         packed = self.__dict__.get("_packed_projection")
         if packed is None or packed[0] != signature:
             weight = torch.cat([p.weight for p in projections])
@@ -117,15 +148,12 @@ class MiraMixer(nn.Module):
         """Whether this call takes the coefficient-forming scan (model/mira_mixer.py:739-760):
         an uncached, gradient-free forward whose coefficient_projection is a plain, unhooked
         nn.Linear, and no positive-pole remapping."""
-        projection = self.coefficient_projection
         return (normalized_x.is_cuda and cache is None and not self.positive_poles
-                and not torch.is_grad_enabled() and type(projection) is nn.Linear
-                and not projection._forward_pre_hooks and not projection._forward_hooks
-                and "forward" not in projection.__dict__)
+                and not torch.is_grad_enabled() and _plain_linear(self.coefficient_projection))
 
     def forward(self, normalized_x, attn_mask=None, cache=None, layer=None):
-        if cache is not None and not (layer is not None and not self.training
-                                      and hasattr(cache, "get")):
+        if cache is not None and not (prefix_cache.enabled() and layer is not None
+                                      and not self.training and hasattr(cache, "get")):
             raise ValueError("streaming cache is not wired into mira-dsp")
         if torch.is_grad_enabled() and (normalized_x.requires_grad or any(
                 p.requires_grad for p in self.parameters())):
@@ -169,11 +197,12 @@ class MiraMixer(nn.Module):
         valid = None if attn_mask is None else attn_mask[:, -tokens:].bool()
         held = None if cache is None else cache.get(layer)
         if tokens == 1 and held is not None:
-            # a decode step on a held state: updated in place, so a step allocates no state
-            # (and a captured step replays on the same tensor)
+            # a decode step on a held state; a cache that opted in (in_place) has it overwritten,
+            # so the step allocates no state and a captured step replays on the same tensor
             result = plugin.matrix_lattice_step(
                 signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
-                raw_beta, held, valid=valid, arch=self.arch, inplace=True)
+                raw_beta, held, valid=valid, arch=self.arch,
+                inplace=bool(getattr(cache, "in_place", False)))
         else:
             result = plugin.matrix_lattice_iir(
                 signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,

@@ -18,7 +18,10 @@ half-precision PyTorch model stores a tensor (every norm, projection, SiLU, scan
 output), so a bf16 model is compared with the same arithmetic rounded at the same places; without
 it everything stays in the working precision.
 
-Pinning (tests/test_stack.py): RMSNorm rows have unit root-mean-square (times the weight) and a
+Pinning (tests/test_stack.py): the reference's own MiraMixer, MiraBlock and 2-layer MiraLLM on
+identical parameters and inputs (tests/golden/stack_*.npz, written by make_golden.py), including
+prompt-then-steps through its PrefixCache, where a dropped control SiLU or a final norm without
+its bias fails; RMSNorm rows have unit root-mean-square (times the weight) and a
 constant row maps to +-1; a mixer whose coefficient projection is zero outputs exactly zero (rho
 routes the readout); a mixer whose coefficients are constants set through the projection bias
 reduces, at K=1 and d_m=1, to the closed-form first-order recurrence (a wrong span order or a
@@ -35,6 +38,12 @@ from . import lattice as L
 
 def silu(x):
     return x / (1.0 + np.exp(-x))
+
+
+def control_activation(x):
+    """SiLU on the control before the coefficient projection (model/mira_mixer.py:694,706); a
+    name of its own so a test can plant its omission."""
+    return silu(x)
 
 
 def _r(rnd, a):
@@ -64,8 +73,8 @@ def mixer_forward(x, p, prefix, order, channels, memory, arch, valid=None, state
     B, T, _ = x.shape
     signal_write = _r(rnd, linear(x, p[prefix + "input_projection.weight"]))
     gamma = _r(rnd, linear(x, p[prefix + "to_gate.weight"], p[prefix + "to_gate.bias"]))
-    control = _r(rnd, silu(_r(rnd, linear(x, p[prefix + "to_control.weight"],
-                                          p[prefix + "to_control.bias"]))))
+    control = _r(rnd, control_activation(_r(rnd, linear(x, p[prefix + "to_control.weight"],
+                                                        p[prefix + "to_control.bias"]))))
     coefficients = _r(rnd, linear(control, p[prefix + "coefficient_projection.weight"],
                                   p[prefix + "coefficient_projection.bias"]))
     signal, raw_write = signal_write[..., :channels], signal_write[..., channels:]

@@ -2,7 +2,9 @@
 
 What this pins that nothing else does: the reference's own float32 rounding of its batched
 per-token formulation, `matrix_lattice_iir` (model/mira_mixer.py:246-387), on identical seeded
-inputs. Stage maps, the K=1 recurrence, the stage loop and the chunk composition are pinned
+inputs; and the layer stack around it -- MiraMixer's projections, control SiLU, split and
+out_proj, MiraBlock's norms and feed-forward, MiraLLM's final norm with bias and tied head, and
+decoding through the reference PrefixCache (`stack_*` fixtures). Stage maps, the K=1 recurrence, the stage loop and the chunk composition are pinned
 independently by closed forms and invariants in tests/test_oracle.py; these vectors pin the
 literal "max abs error against the reference's CPU mixer" criterion.
 
@@ -41,6 +43,8 @@ def cases():
                 dict(B=1, T=300, C=8, K=2, M=16, arch="cauchy_x_hyperbolic", mask=False,
                      state=False, seed=3, beta_bias=0.0, alpha_bias=0.5)))
     out.append(("diag_cfg1_reduced", "diag", dict(B=1, T=512, D=32, seed=4)))
+    for arch in ("cauchy_x_hyperbolic", "expsoftplus_x_mobius"):
+        out.append((f"stack_{arch}", "stack", dict(arch=arch, seed=6)))
     out.append(("gla_cfg3_reduced", "gla", dict(B=1, T=96, H=2, dk=16, dv=16, seed=5)))
     return out
 
@@ -89,6 +93,9 @@ def run(reference_root):
             inputs = Bl.diag_as_lattice(u, a, h0)
             y, final = reference(*inputs[:7], None, inputs[7], "cauchy_x_hyperbolic")
             arrays = dict(x=x, a=a, w=w, bias=bias, h0=h0, u=u, y=y, final=final)
+        elif kind == "stack":
+            arrays = stack_case(torch, reference_root, rng, p["arch"])
+            y = arrays["llm_logits"]
         else:
             q, k, v, g = Bl.gla_inputs(rng, p["B"], p["T"], p["H"], p["dk"], p["dv"])
             S0 = (rng.standard_normal((p["B"], p["H"], p["dv"], p["dk"])) * 0.1).astype(np.float32)
@@ -97,6 +104,58 @@ def run(reference_root):
             arrays = dict(q=q, k=k, v=v, g=g, S0=S0, y=y, final=final)
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **arrays)
         print(f"{name}: y {y.shape} max|y| {np.abs(y).max():.4g}", flush=True)
+
+
+STACK = dict(vocab_size=40, n_layer=2, n_embd=24, lattice_d_e=12, lattice_order=2,
+             coefficient_bottleneck=6, memory_dimension=4, ffn_hidden=32)
+
+
+def stack_case(torch, reference_root, rng, arch):
+    """The reference's MiraMixer, MiraBlock and a 2-layer MiraLLM (model/mira_mixer.py:544-856,
+    model/mira_block.py:156-205, model/mira_llm.py:20-364) on the CPU in float32, eval mode, with
+    every parameter redrawn from `rng` (so the coefficient projection, the control SiLU, the FFN,
+    the final norm's bias and the tied head all move the outputs). Saved: the LLM's parameters
+    under their state_dict names (`p.<name>`), token ids, a padding mask, the mixer / block /
+    LLM outputs, and the logits of the same ids fed as a prompt then one token at a time through
+    the reference PrefixCache (`steps_logits`)."""
+    llm_module = __import__("model.mira_llm", fromlist=["MiraLLM"])
+    cache_module = __import__("model.prefix_cache", fromlist=["PrefixCache"])
+    modulus, argument = arch.split("_x_")
+    torch.manual_seed(0)
+    model = llm_module.MiraLLM(lattice_modulus_map=modulus, lattice_argument_map=argument,
+                               **STACK).eval()
+    with torch.no_grad():
+        for name, parameter in model.named_parameters():
+            scale = 0.1 if name.endswith(("rn1.weight", "rn2.weight", "lnf.weight")) else 0.3
+            value = rng.standard_normal(tuple(parameter.shape)) * scale
+            if name.endswith(("rn1.weight", "rn2.weight", "lnf.weight")):
+                value = value + 1.0
+            parameter.copy_(torch.from_numpy(value.astype(np.float32)))
+    B, T, prompt = 2, 11, 6
+    ids = rng.integers(0, STACK["vocab_size"], size=(B, T))
+    mask = np.ones((B, T), dtype=bool)
+    mask[0, :2] = False                       # left padding on the first row
+    mask[1, 7] = False                        # and one masked token inside the second
+    d = STACK["n_embd"]
+    hidden = rng.standard_normal((B, T, d)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    with torch.no_grad():
+        block = model.blocks[0]
+        mixer_out = block.mixer(block.rn1(t(hidden)), t(mask))
+        block_out = block(t(hidden), t(mask))
+        logits = model(t(ids), attention_mask=t(mask)).logits
+        cache = cache_module.PrefixCache(STACK["n_layer"], budget=0)
+        steps = [model(t(ids[:, :prompt]), cache=cache).logits]
+        for i in range(prompt, T):
+            steps.append(model(t(ids[:, i:i + 1]), cache=cache).logits)
+        steps_logits = torch.cat(steps, dim=1)
+    arrays = {f"p.{name}": value.detach().numpy().copy()
+              for name, value in model.state_dict().items()}
+    arrays.update(ids=ids.astype(np.int64), mask=mask, hidden=hidden,
+                  mixer_out=mixer_out.numpy(), block_out=block_out.numpy(),
+                  llm_logits=logits.numpy(), steps_logits=steps_logits.numpy(), prompt=prompt,
+                  arch=np.array(arch))
+    return arrays
 
 
 if __name__ == "__main__":

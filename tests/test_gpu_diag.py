@@ -221,3 +221,40 @@ def test_reference_path_realisation_matches(torch_mod, plugin):
     _check(to_numpy(y), to_numpy(out) / 32.0, "float32", "kernel vs lattice realisation")
     ref, _ = L.lattice_scan_batched(*lat[:7], state=lat[7])
     _check(to_numpy(y), ref / 32.0, "float32", "kernel vs oracle of the reference path")
+
+
+def test_look_back_prefill_refuses_graph_capture(torch_mod, plugin):
+    """The look-back form (a batch too narrow for one column per half of the CUs) tags its
+    records with a per-launch epoch passed as a kernel argument, which a graph would freeze:
+    the library refuses capture (ValueError) instead of replaying stale records. The column
+    form takes no epoch and captures normally."""
+    torch = torch_mod
+    rng = np.random.default_rng(21)
+    x, a, w, _, _ = Bl.diag_inputs(rng, 1, 96, 256)
+    xd, ad, wd = to_device(x), to_device(a), to_device(w)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = plugin.diag_conv_scan(xd, ad, wd)          # allocates this stream's workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(ValueError, match="captured"):
+        with torch.cuda.graph(graph, stream=side):
+            plugin.diag_conv_scan(xd, ad, wd)
+    torch.cuda.synchronize()
+    want, _, _ = _oracle(x, a, w, torch=torch)
+    _check(to_numpy(eager), want, "float32", "eager look-back prefill")
+    # a batch wide enough for the column form is captured and replayed like any kernel
+    x2, a2, w2, _, _ = Bl.diag_inputs(rng, 8, 40, 2048)
+    xd2, ad2, wd2 = to_device(x2), to_device(a2), to_device(w2)
+    with torch.cuda.stream(side):
+        plugin.diag_conv_scan(xd2, ad2, wd2)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        captured = plugin.diag_conv_scan(xd2, ad2, wd2)
+    want2, _, _ = _oracle(x2, a2, w2, torch=torch)
+    for _ in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(to_numpy(captured), want2, "float32", "captured column prefill")

@@ -4,10 +4,12 @@ in float32 and bfloat16 (the oracle rounding to bf16 wherever the bf16 model sto
 with a padding mask; and a prompt followed by single-token steps through
 a PrefixCache against the one-shot forward (the kv_cache.check invariant of
 helpers/kv_cache.py:196-233 applied to the whole model)."""
+import os
+
 import numpy as np
 import pytest
 
-from _util import FP32_SCALED, HALF_SCALED, scaled
+from _util import FP32_SCALED, HALF_SCALED, golden_files, max_abs, scaled
 from oracle import stack as St
 
 pytestmark = pytest.mark.gpu
@@ -92,6 +94,65 @@ def test_prompt_then_steps_equals_one_shot(torch_mod, model_cls):
     assert len(cache) == 26
     error = scaled(torch.cat(parts, dim=1).cpu().numpy(), full.cpu().numpy())
     assert error <= 1e-5, f"stepped vs one-shot: scaled error {error:.3e}"
+
+
+STACK_FIXTURES = golden_files("stack_")
+
+
+@pytest.mark.parametrize("path", STACK_FIXTURES, ids=os.path.basename)
+def test_hip_stack_matches_the_reference_fixtures(torch_mod, model_cls, path):
+    """The reference's own MiraMixer, MiraBlock and 2-layer MiraLLM outputs (CPU, float32, written
+    by tests/golden/make_golden.py) against mira_amd's modules on the GPU in float32 with the
+    same state_dict: the mixer with a padding mask, the block, the LLM logits, and prompt-then-
+    steps through a PrefixCache. Bound: max abs error <= 1e-5 x max(1, largest magnitude)."""
+    torch = torch_mod
+    from mira_amd.prefix_cache import PrefixCache
+
+    f = np.load(path, allow_pickle=False)
+    cfg = dict(vocab_size=40, n_layer=2, n_embd=24, lattice_d_e=12, lattice_order=2,
+               coefficient_bottleneck=6, memory_dimension=4, ffn_hidden=32, arch=str(f["arch"]))
+    model = model_cls(**cfg)
+    model.load_state_dict({k[2:]: torch.from_numpy(f[k].copy()) for k in f.files
+                           if k.startswith("p.")}, strict=True)
+    model = model.to("cuda").eval()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")  # noqa: E731
+    ids, mask, prompt = t(f["ids"]), t(f["mask"]), int(f["prompt"])
+    with torch.no_grad():
+        block = model.blocks[0]
+        got = dict(mixer_out=block.mixer(block.rn1(t(f["hidden"])), mask),
+                   block_out=block(t(f["hidden"]), mask),
+                   llm_logits=model(ids, attention_mask=mask).logits)
+        cache = PrefixCache(cfg["n_layer"], budget=0)
+        parts = [model(ids[:, :prompt], cache=cache).logits]
+        for i in range(prompt, ids.shape[1]):
+            parts.append(model(ids[:, i:i + 1], cache=cache).logits)
+        got["steps_logits"] = torch.cat(parts, dim=1)
+    for name, value in got.items():
+        want = f[name]
+        error = max_abs(value.float().cpu().numpy(), want)
+        assert error <= 1e-5 * max(1.0, float(np.abs(want).max())), f"{name}: {error:.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_fused_rms_norm_is_bit_identical_to_the_stepwise_form(torch_mod, dtype):
+    """mira_amd.block.RMSNorm runs PyTorch's fused rms_norm where the weight has the input's
+    dtype; that is bit-for-bit the reference's stepwise float32 form (model/mira_block.py:28-35)
+    on the GPU, for bf16 and fp32 rows of several widths."""
+    torch = torch_mod
+    from mira_amd.block import RMSNorm
+
+    kind = getattr(torch, dtype)
+    torch.manual_seed(11)
+    for width in (24, 64, 2048):
+        norm = RMSNorm(width).to("cuda", kind)
+        with torch.no_grad():
+            norm.weight.normal_(1.0, 0.2)
+            x = (torch.randn(4, 33, width, device="cuda") * 3.0).to(kind)
+            fused = norm(x)
+            z = x.float()
+            stepwise = (z * torch.rsqrt(z.square().mean(dim=-1, keepdim=True) + norm.eps)
+                        * norm.weight.float()).to(kind)
+        assert torch.equal(fused, stepwise), f"{dtype} width {width}"
 
 
 def test_gradients_are_refused_not_dropped(torch_mod, model_cls):

@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 import torch
 
-from mira_amd import hardware, mira
+from mira_amd import config, hardware, mira, prefix_cache
+from mira_amd.llm import MiraLLM
 from mira_amd.mixer import MiraMixer
 from mira_amd.prefix_cache import PrefixCache, affordable, state_bytes
 from oracle import lattice as L
@@ -81,3 +82,103 @@ def test_mixer_layout_and_cpu_refusal():
         MiraMixer(32, arch="nope")
     with pytest.raises(ValueError):
         mixer.train()(torch.zeros(1, 3, 32), cache=PrefixCache(1), layer=0)
+
+
+def test_prefix_cache_switch_and_configured_budget(monkeypatch):
+    """INFERENCE["prefix_cache"] = 0 makes the mixer refuse a cache (model/mira_mixer.py:726-729);
+    the default ceiling is INFERENCE["prefix_cache_size"] GiB, read at call time
+    (model/prefix_cache.py:47-64)."""
+    monkeypatch.setitem(config.INFERENCE, "prefix_cache_size", 0.5)
+    assert PrefixCache(2).budget == 1 << 29
+    assert PrefixCache(2, budget=0).budget == 0
+    assert affordable(1, 1, 1, 1 << 20, 256)[0] is False           # 1 GiB > 0.5 GiB
+    assert affordable(1, 1, 1, 1 << 20, 64)[0] is True
+    assert "GiB" in prefix_cache.describe(24, 4, 2, 2048, 64)
+    mixer = MiraMixer(32, lattice_order=2, d_e=24, coefficient_bottleneck=8,
+                      memory_dimension=16).eval()
+    monkeypatch.setitem(config.INFERENCE, "prefix_cache", 0)
+    assert not prefix_cache.enabled()
+    with pytest.raises(ValueError, match="not wired"):
+        with torch.no_grad():
+            mixer(torch.zeros(1, 3, 32), cache=PrefixCache(1), layer=0)
+
+
+def test_prefix_cache_reset_through_model():
+    model = MiraLLM(vocab_size=17, n_layer=2, n_embd=16, lattice_d_e=8, memory_dimension=4)
+    cache = PrefixCache(2)
+    cache.put(0, torch.ones(1, 2, 8, 4))
+    cache.advance(3)
+    cache.key_valid = torch.ones(1, 3, dtype=torch.bool)
+    cache.reset(model)
+    assert cache.state == [None, None] and len(cache) == 0 and cache.key_valid is None
+
+
+def test_prefix_cache_keeps_earlier_states_unless_in_place():
+    """put() swaps in a new tensor; a caller holding an earlier state sees it unchanged. Only a
+    cache that opts in (in_place) has its held tensor overwritten by single-token steps."""
+    cache = PrefixCache(1)
+    assert cache.in_place is False
+    first = cache.put(0, torch.zeros(1, 1, 2, 2))
+    second = cache.put(0, torch.ones(1, 1, 2, 2))
+    assert first is not second and float(first.sum()) == 0.0
+
+
+def _projection_mixer():
+    torch.manual_seed(0)
+    return MiraMixer(32, lattice_order=2, d_e=24, coefficient_bottleneck=8,
+                     memory_dimension=16).eval()
+
+
+def test_packed_projection_matches_module_calls():
+    mixer = _projection_mixer()
+    x = torch.randn(2, 5, 32)
+    with torch.no_grad():
+        packed = mixer.project_recurrence_inputs(x)
+        assert "_packed_projection" in mixer.__dict__
+    unpacked = (mixer.input_projection(x), mixer.coefficient_projection(
+        torch.nn.functional.silu(mixer.to_control(x))), mixer.to_gate(x))
+    for got, want in zip(packed, unpacked):
+        torch.testing.assert_close(got, want.detach(), rtol=1e-5, atol=1e-6)
+
+
+def test_packed_projection_respects_hooks_and_subclasses():
+    """A forward hook on to_gate, a global hook or a Linear subclass must change what the
+    inference projection returns exactly as calling the modules would (model/mira_mixer.py:
+    664-672); the packed GEMM is skipped for them."""
+    x = torch.randn(2, 5, 32)
+    mixer = _projection_mixer()
+    with torch.no_grad():
+        base = mixer.project_recurrence_inputs(x)[2]
+        handle = mixer.to_gate.register_forward_hook(lambda module, args, out: out * 3.0)
+        hooked = mixer.project_recurrence_inputs(x)[2]
+        handle.remove()
+        torch.testing.assert_close(hooked, base * 3.0)
+        handle = torch.nn.modules.module.register_module_forward_hook(
+            lambda module, args, out: out + 1.0 if module is mixer.to_gate else None)
+        try:
+            globally = mixer.project_recurrence_inputs(x)[2]
+        finally:
+            handle.remove()
+        torch.testing.assert_close(globally, base + 1.0)
+
+    class Doubled(torch.nn.Linear):
+        def forward(self, value):
+            return 2.0 * super().forward(value)
+
+    replacement = Doubled(32, mixer.to_gate.out_features)
+    replacement.load_state_dict(mixer.to_gate.state_dict())
+    mixer.to_gate = replacement
+    with torch.no_grad():
+        torch.testing.assert_close(mixer.project_recurrence_inputs(x)[2], base * 2.0)
+
+
+def test_packed_projection_rebuilds_on_parameter_change():
+    mixer = _projection_mixer()
+    x = torch.randn(1, 3, 32)
+    with torch.no_grad():
+        before = mixer.project_recurrence_inputs(x)[2]
+        mixer.to_gate.weight.mul_(0.5)                      # in place: _version moves
+        mixer.to_gate.bias.zero_()
+        after = mixer.project_recurrence_inputs(x)[2]
+    assert not torch.equal(after, before)
+    torch.testing.assert_close(after, mixer.to_gate(x))

@@ -1,10 +1,87 @@
 """CPU checks of the layer stack around the scan: the oracle's RMSNorm / mixer / block / LLM
 restatement (oracle/stack.py) pinned against closed forms and invariants, and the host modules
 (mira_amd.block, mira_amd.llm) against the oracle where they need no GPU."""
+import os
+
 import numpy as np
 import pytest
 
+from _util import golden_files, scaled
 from oracle import stack as St
+
+STACK_FIXTURES = golden_files("stack_")
+STACK_CFG = dict(vocab_size=40, n_layer=2, n_embd=24, lattice_d_e=12, lattice_order=2,
+                 coefficient_bottleneck=6, memory_dimension=4, ffn_hidden=32)
+# the oracle in float64 against the reference's float32 modules: a few float32 roundings apart
+FIXTURE_SCALED = 1e-5
+
+
+def _fixture(path):
+    f = np.load(path, allow_pickle=False)
+    params = {k[2:]: f[k].astype(np.float64) for k in f.files if k.startswith("p.")}
+    return f, params, dict(STACK_CFG, arch=str(f["arch"]))
+
+
+def _oracle_outputs(f, p, cfg):
+    mask = f["mask"]
+    hidden = f["hidden"].astype(np.float64)
+    pre = "blocks.0."
+    mixer, _ = St.mixer_forward(St.rmsnorm(hidden, p[pre + "rn1.weight"]), p, pre + "mixer.",
+                                cfg["lattice_order"], cfg["lattice_d_e"],
+                                cfg["memory_dimension"], cfg["arch"], valid=mask)
+    block, _ = St.block_forward(hidden, p, pre, cfg, valid=mask)
+    logits, _ = St.llm_forward(f["ids"], p, cfg, valid=mask)
+    prompt = int(f["prompt"])
+    ids = f["ids"]
+    parts, states = [], None
+    first, states = St.llm_forward(ids[:, :prompt], p, cfg)
+    parts.append(first)
+    for t in range(prompt, ids.shape[1]):
+        step, states = St.llm_forward(ids[:, t:t + 1], p, cfg, states=states)
+        parts.append(step)
+    return dict(mixer_out=mixer, block_out=block, llm_logits=logits,
+                steps_logits=np.concatenate(parts, axis=1))
+
+
+@pytest.mark.parametrize("path", STACK_FIXTURES, ids=os.path.basename)
+def test_oracle_matches_the_reference_stack(path):
+    """The reference's MiraMixer, MiraBlock and 2-layer MiraLLM (model/mira_mixer.py:657-856,
+    model/mira_block.py:21-48,203-205, model/mira_llm.py:225-351) on the CPU, with a nonzero
+    coefficient projection, a padding mask and prompt-then-steps through its PrefixCache."""
+    f, p, cfg = _fixture(path)
+    for name, got in _oracle_outputs(f, p, cfg).items():
+        error = scaled(got, f[name])
+        assert error <= FIXTURE_SCALED, f"{name}: scaled error {error:.3e}"
+
+
+def test_planted_stack_mistakes_are_caught(monkeypatch):
+    """A control without its SiLU, or a final norm without its bias, misses the reference's
+    logits by far more than the tolerance."""
+    f, p, cfg = _fixture(STACK_FIXTURES[0])
+    mask = f["mask"]
+    monkeypatch.setattr(St, "control_activation", lambda x: x)
+    no_silu, _ = St.llm_forward(f["ids"], p, cfg, valid=mask)
+    monkeypatch.undo()
+    assert scaled(no_silu, f["llm_logits"]) > 100 * FIXTURE_SCALED
+    no_bias = dict(p, **{"lnf.bias": np.zeros_like(p["lnf.bias"])})
+    dropped, _ = St.llm_forward(f["ids"], no_bias, cfg, valid=mask)
+    assert scaled(dropped, f["llm_logits"]) > 100 * FIXTURE_SCALED
+    untied = dict(p, **{"head.weight": p["head.weight"][::-1].copy()})
+    wrong_head, _ = St.llm_forward(f["ids"], untied, cfg, valid=mask)
+    assert scaled(wrong_head, f["llm_logits"]) > 100 * FIXTURE_SCALED
+
+
+def test_host_model_loads_the_reference_state_dict():
+    """A reference MiraLLM state_dict (names and shapes, the tied head and the unused mask
+    embedding included) loads into mira_amd.llm.MiraLLM without a missing or extra key."""
+    torch = pytest.importorskip("torch")
+    from mira_amd.llm import MiraLLM
+
+    f, _, cfg = _fixture(STACK_FIXTURES[0])
+    model = MiraLLM(**cfg)
+    state = {k[2:]: torch.from_numpy(f[k].copy()) for k in f.files if k.startswith("p.")}
+    model.load_state_dict(state, strict=True)
+    assert model.tok.weight is model.head.weight
 
 
 def _params(rng, cfg, scale=0.3):
