@@ -29,8 +29,11 @@ class RMSNorm(nn.Module):
         self.eps = float(eps)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.bias is None and self.weight.dtype == x.dtype:
-            # one fused kernel that computes in float32 and rounds once, as the steps below do
+        if self.bias is None and x.dtype == torch.bfloat16 and self.weight.dtype == x.dtype:
+            # one fused kernel that computes in float32 and rounds once to bf16 (2.7 ms of a
+            # 40 ms cfg5 forward saved). Its float32 sum runs in another order than the steps
+            # below, so a few bf16 outputs in 10^5 land one bf16 ulp away; float32 rows would
+            # differ by an ulp in a third of the outputs, so float32 takes the steps.
             return F.rms_norm(x, (x.shape[-1],), self.weight, self.eps)
         z = x.float()
         z = z * torch.rsqrt(z.square().mean(dim=-1, keepdim=True) + self.eps) * self.weight.float()

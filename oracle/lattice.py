@@ -350,3 +350,129 @@ def random_inputs(rng, B, T, C, K, M, dtype=np.float32, scale=(0.15, 0.12, 0.15,
     values[1] = (values[1] + dtype(alpha_bias)).astype(dtype)
     values[6] = (values[6] + dtype(beta_bias)).astype(dtype)
     return values
+
+
+# --------------------------------------------------------------------------------------------
+# the backward: gradients of the scan's output with respect to all seven inputs
+#     what autograd returns through model/mira_mixer.py:246-387 (and the plugin's
+#     MatrixLatticeIIR.backward, kernel/cuda/mira_dspv2/mira.py:1295-1433)
+# --------------------------------------------------------------------------------------------
+def stage_map_derivatives(alpha, beta, arch):
+    """(cos, sin, r, dcos/dalpha, dsin/dalpha, dr/dbeta), float64, of the stage maps
+    (model/mira_mixer.py:56-145), with the derivatives autograd forms there: the reciprocal
+    branches of the rational maps give the same closed forms; hyperbolic's |alpha| has slope 0
+    at 0 (so d sech = -sech tanh, also 0 there); expexp's ceiling stops the gradient above 80."""
+    a = np.asarray(alpha, np.float64)
+    b = np.asarray(beta, np.float64)
+    radius_name, rotation_name = arch.split("_x_")
+    if rotation_name == "mobius":
+        denominator = 1.0 + a * a
+        cos, sin = 2 * a / denominator, (1 - a * a) / denominator
+        dcos, dsin = 2 * (1 - a * a) / denominator ** 2, -4 * a / denominator ** 2
+    elif rotation_name == "hyperbolic":
+        cos, sin = 1.0 / np.cosh(a), np.tanh(a)
+        dcos, dsin = -cos * sin, cos * cos
+    else:
+        cos, sin = np.cos(a), np.sin(a)
+        dcos, dsin = -sin, cos
+    if radius_name == "cauchy":
+        r = 1.0 / (1.0 + b * b)
+        dr = -2 * b * r * r
+    elif radius_name == "gaussian":
+        r = np.exp(-b * b)
+        dr = -2 * b * r
+    elif radius_name == "expexp":
+        capped = np.minimum(b, EXPEXP_BETA_CEILING)
+        r = np.exp(-np.exp(capped))
+        dr = np.where(b <= EXPEXP_BETA_CEILING, -np.exp(capped) * r, 0.0)
+    elif radius_name == "expsoftplus":
+        r = 1.0 / (1.0 + np.exp(b))
+        dr = -r * (1 - r)
+    else:
+        q = b * b
+        r = q / (1 + q)
+        dr = 2 * b / (1 + q) ** 2
+    return cos, sin, r, dcos, dsin, dr
+
+
+def silu_derivative(value):
+    """d/dx x sigmoid(x) = sigmoid(x) (1 + x (1 - sigmoid(x)))."""
+    sigma = 1.0 / (1.0 + np.exp(-np.asarray(value, np.float64)))
+    return sigma * (1.0 + value * (1.0 - sigma))
+
+
+def lattice_backward(x, alpha, rho, gamma, write, read, beta, grad_out, valid=None,
+                     arch="cauchy_x_hyperbolic"):
+    """Gradients (dx, dalpha, dbeta, drho, dgamma, dwrite, dread) of sum(grad_out * y) for
+    y = matrix_lattice_iir(...) from a zero state, in float64, by the explicit adjoint of the
+    stage loop. With lambda the adjoint of the carried state V_t and
+    Lambda_k = lambda_t[k] (k < K) + g rho_k nu_k dy (the readout's share), a token runs its
+    stages backward (k = 1..K) from dU = Lambda_0:
+        d rs_k += Lambda_k U_in - dU V_(t-1)[k-1],   d rc_k += Lambda_k V_(t-1)[k-1] + dU U_in,
+        lambda_(t-1)[k-1] = rc_k Lambda_k - rs_k dU,  dU <- rs_k Lambda_k + rc_k dU,
+    ending at dU = d(x s): dx = sum_m dU s, ds = sum_c dU x. rc = r cos and rs = r sin chain to
+    alpha and beta through stage_map_derivatives. A masked token passes lambda through and gets
+    zero gradients."""
+    B, T, C, K, M = _check_shapes(x, alpha, rho, gamma, write, read, beta, valid, None)
+    f64 = np.float64
+    x, rho, gamma, write, read, dy = _cast(f64, x, rho, gamma, write, read, grad_out)
+    cos, sin, r, dcos, dsin, dr = stage_map_derivatives(alpha, beta, arch)
+    rc, rs = r * cos, r * sin                                    # [B,T,C,K], stage k at k-1
+    gate = gamma / (1.0 + np.exp(-gamma))
+    dgate = silu_derivative(gamma)
+    keep = np.ones((B, T), bool) if valid is None else np.asarray(valid, bool)
+    # forward, keeping the state entering every token
+    entering = np.zeros((T, B, K, C, M))
+    V = np.zeros((B, K, C, M))
+    for t in range(T):
+        entering[t] = V
+        U = x[:, t, :, None] * write[:, t, None, :]
+        levels = [None] * (K + 1)
+        for k in range(K, 0, -1):
+            delayed = V[:, k - 1]
+            levels[k] = rs[:, t, :, k - 1, None] * U + rc[:, t, :, k - 1, None] * delayed
+            U = rc[:, t, :, k - 1, None] * U - rs[:, t, :, k - 1, None] * delayed
+        levels[0] = U
+        V = np.where(keep[:, t, None, None, None], np.stack(levels[:K], axis=1), V)
+    grads = dict(x=np.zeros((B, T, C)), alpha=np.zeros((B, T, C, K)), beta=np.zeros((B, T, C, K)),
+                 rho=np.zeros((B, T, C, K + 1)), gamma=np.zeros((B, T, C)),
+                 write=np.zeros((B, T, M)), read=np.zeros((B, T, K + 1, M)))
+    lam = np.zeros((B, K, C, M))
+    for t in range(T - 1, -1, -1):
+        Vp = entering[t]
+        U = x[:, t, :, None] * write[:, t, None, :]
+        U_in = [None] * (K + 1)
+        levels = [None] * (K + 1)
+        for k in range(K, 0, -1):
+            U_in[k] = U
+            delayed = Vp[:, k - 1]
+            levels[k] = rs[:, t, :, k - 1, None] * U + rc[:, t, :, k - 1, None] * delayed
+            U = rc[:, t, :, k - 1, None] * U - rs[:, t, :, k - 1, None] * delayed
+        levels[0] = U
+        e = dy[:, t] * gate[:, t]                                             # [B,C]
+        P = np.stack([(levels[k] * read[:, t, k, None, :]).sum(-1) for k in range(K + 1)], -1)
+        weight = e[..., None] * rho[:, t]                                     # e rho_k, [B,C,K+1]
+        Lam = [weight[..., k, None] * read[:, t, k, None, :]
+               + (lam[:, k] if k < K else 0.0) for k in range(K + 1)]
+        dU = Lam[0]
+        drc, drs = np.zeros((B, C, K)), np.zeros((B, C, K))
+        lam_new = np.zeros_like(lam)
+        for k in range(1, K + 1):
+            delayed = Vp[:, k - 1]
+            drs[..., k - 1] = (Lam[k] * U_in[k] - dU * delayed).sum(-1)
+            drc[..., k - 1] = (Lam[k] * delayed + dU * U_in[k]).sum(-1)
+            lam_new[:, k - 1] = rc[:, t, :, k - 1, None] * Lam[k] - rs[:, t, :, k - 1, None] * dU
+            dU = rs[:, t, :, k - 1, None] * Lam[k] + rc[:, t, :, k - 1, None] * dU
+        on = keep[:, t]
+        w = on[:, None].astype(f64)
+        grads["x"][:, t] = w * (dU * write[:, t, None, :]).sum(-1)
+        grads["write"][:, t] = on[:, None] * (dU * x[:, t, :, None]).sum(1)
+        grads["rho"][:, t] = w[..., None] * e[..., None] * P
+        grads["gamma"][:, t] = w * dy[:, t] * dgate[:, t] * (rho[:, t] * P).sum(-1)
+        grads["read"][:, t] = on[:, None, None] * np.stack(
+            [(weight[..., k, None] * levels[k]).sum(1) for k in range(K + 1)], 1)
+        grads["alpha"][:, t] = w[..., None] * r[:, t] * (drc * dcos[:, t] + drs * dsin[:, t])
+        grads["beta"][:, t] = w[..., None] * dr[:, t] * (drc * cos[:, t] + drs * sin[:, t])
+        lam = np.where(on[:, None, None, None], lam_new, lam)
+    return (grads["x"], grads["alpha"], grads["beta"], grads["rho"], grads["gamma"],
+            grads["write"], grads["read"])

@@ -45,6 +45,14 @@ def cases():
     out.append(("diag_cfg1_reduced", "diag", dict(B=1, T=512, D=32, seed=4)))
     for arch in ("cauchy_x_hyperbolic", "expsoftplus_x_mobius"):
         out.append((f"stack_{arch}", "stack", dict(arch=arch, seed=6)))
+    for arch in L.ARCH_STAGE:
+        out.append((f"grad_k2m16_{arch}", "grad",
+                    dict(B=2, T=45, C=5, K=2, M=16, arch=arch, mask=True, seed=7)))
+    for K, M, arch in ((1, 8, "cauchy_x_mobius"), (4, 8, "expsoftplus_x_hyperbolic"),
+                       (2, 64, "cauchy_x_hyperbolic"), (8, 16, "gaussian_x_identity"),
+                       (2, 32, "hill_x_mobius")):
+        out.append((f"grad_k{K}m{M}_{arch}", "grad",
+                    dict(B=2, T=70, C=6, K=K, M=M, arch=arch, mask=False, seed=8)))
     out.append(("gla_cfg3_reduced", "gla", dict(B=1, T=96, H=2, dk=16, dv=16, seed=5)))
     return out
 
@@ -93,6 +101,9 @@ def run(reference_root):
             inputs = Bl.diag_as_lattice(u, a, h0)
             y, final = reference(*inputs[:7], None, inputs[7], "cauchy_x_hyperbolic")
             arrays = dict(x=x, a=a, w=w, bias=bias, h0=h0, u=u, y=y, final=final)
+        elif kind == "grad":
+            arrays = grad_case(torch, mixer, L, rng, p)
+            y = arrays["y"]
         elif kind == "stack":
             arrays = stack_case(torch, reference_root, rng, p["arch"])
             y = arrays["llm_logits"]
@@ -104,6 +115,31 @@ def run(reference_root):
             arrays = dict(q=q, k=k, v=v, g=g, S0=S0, y=y, final=final)
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **arrays)
         print(f"{name}: y {y.shape} max|y| {np.abs(y).max():.4g}", flush=True)
+
+
+def grad_case(torch, mixer, L, rng, p):
+    """Gradients of sum(dy * y) through the reference's `matrix_lattice_iir` on the CPU in
+    float32 (autograd through its checkpointed per-token chunks, model/mira_mixer.py:246-387):
+    what the plugin's MatrixLatticeIIR.backward must return (kernel/cuda/mira_dspv2/check.py:
+    42-104 compares against exactly this). Inputs drawn as the reference harness draws them
+    (check.py:52-69), from a zero state."""
+    B, T, C, K, M = p["B"], p["T"], p["C"], p["K"], p["M"]
+    values = L.random_inputs(rng, B, T, C, K, M)
+    valid = (rng.random((B, T)) > 0.25) if p["mask"] else None
+    dy = rng.standard_normal((B, T, C)).astype(np.float32)
+    tensors = [torch.from_numpy(np.ascontiguousarray(v)).requires_grad_(True) for v in values]
+    x, alpha, rho, gamma, write, read, beta = tensors
+    y = mixer.matrix_lattice_iir(x, alpha, rho, gamma, write, read,
+                                 valid=None if valid is None else torch.from_numpy(valid),
+                                 raw_beta=beta, arch=p["arch"])
+    (y * torch.from_numpy(dy)).sum().backward()
+    names = ("x", "alpha", "rho", "gamma", "write", "read", "beta")
+    arrays = {name: value for name, value in zip(names, values)}
+    arrays.update({f"d{name}": tensor.grad.numpy().copy() for name, tensor in zip(names, tensors)})
+    arrays.update(y=y.detach().numpy(), dy=dy, arch=np.array(p["arch"]))
+    if valid is not None:
+        arrays["valid"] = valid
+    return arrays
 
 
 STACK = dict(vocab_size=40, n_layer=2, n_embd=24, lattice_d_e=12, lattice_order=2,

@@ -134,25 +134,34 @@ def test_hip_stack_matches_the_reference_fixtures(torch_mod, model_cls, path):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_fused_rms_norm_is_bit_identical_to_the_stepwise_form(torch_mod, dtype):
-    """mira_amd.block.RMSNorm runs PyTorch's fused rms_norm where the weight has the input's
-    dtype; that is bit-for-bit the reference's stepwise float32 form (model/mira_block.py:28-35)
-    on the GPU, for bf16 and fp32 rows of several widths."""
+def test_rms_norm_against_the_stepwise_form(torch_mod, dtype):
+    """mira_amd.block.RMSNorm against the reference's stepwise float32 form
+    (model/mira_block.py:28-35) on the GPU: float32 runs those steps, so it is bit-identical;
+    bf16 runs PyTorch's fused rms_norm, whose sum of squares is ordered differently, so a few
+    outputs in 10^4 may land one bf16 ulp away and none further."""
     torch = torch_mod
     from mira_amd.block import RMSNorm
 
     kind = getattr(torch, dtype)
     torch.manual_seed(11)
-    for width in (24, 64, 2048):
+    for width in (24, 64, 2048, 4096):
         norm = RMSNorm(width).to("cuda", kind)
         with torch.no_grad():
             norm.weight.normal_(1.0, 0.2)
             x = (torch.randn(4, 33, width, device="cuda") * 3.0).to(kind)
-            fused = norm(x)
+            got = norm(x)
             z = x.float()
             stepwise = (z * torch.rsqrt(z.square().mean(dim=-1, keepdim=True) + norm.eps)
                         * norm.weight.float()).to(kind)
-        assert torch.equal(fused, stepwise), f"{dtype} width {width}"
+        if dtype == "float32":
+            assert torch.equal(got, stepwise), f"width {width}"
+            continue
+        differ = got != stepwise
+        ulp = torch.finfo(kind).eps * stepwise.float().abs().clamp_min(
+            torch.finfo(kind).tiny)
+        gap = (got.float() - stepwise.float()).abs()
+        assert int(differ.sum()) <= max(1, differ.numel() // 10_000), f"width {width}"
+        assert bool((gap <= ulp).all()), f"width {width}: a gap over one bf16 ulp"
 
 
 def test_gradients_are_refused_not_dropped(torch_mod, model_cls):

@@ -7,7 +7,7 @@ import os
 import numpy as np
 import pytest
 
-from _util import golden_files, max_abs, scaled
+from _util import GOLDEN, golden_files, max_abs, scaled
 from oracle import baseline as Bl
 from oracle import lattice as L
 
@@ -322,3 +322,78 @@ def test_planted_mistakes_are_caught(mistake):
     y, _ = scan(*args, valid=None, state=d["state"].astype(F64))
     ref, _ = L.lattice_scan_sequential(*args, valid=None, state=d["state"].astype(F64), dtype=F64)
     assert scaled(y, ref) > 1e-3, f"planted {mistake} went unnoticed"
+
+
+# ---------------------------------------------------------------------------------------------
+# the backward (gradients of the scan), pinned by the reference's own autograd and by fp64
+# finite differences
+# ---------------------------------------------------------------------------------------------
+GRAD_NAMES = ("x", "alpha", "beta", "rho", "gamma", "write", "read")
+GRAD_FIXTURES = golden_files("grad_")
+
+
+def _grad_fixture(path):
+    f = np.load(path, allow_pickle=False)
+    valid = f["valid"] if "valid" in f.files else None
+    inputs = [f[n] for n in ("x", "alpha", "rho", "gamma", "write", "read", "beta")]
+    return f, inputs, valid
+
+
+@pytest.mark.parametrize("path", GRAD_FIXTURES, ids=os.path.basename)
+def test_backward_matches_reference_autograd(path):
+    """Gradients of sum(dy * y) for every input against autograd through the reference's
+    float32 matrix_lattice_iir (model/mira_mixer.py:246-387; tests/golden/grad_*.npz): all 15
+    stage maps at K=2 d_m=16 with a mask, and K/d_m from 1/8 to 8/16."""
+    f, inputs, valid = _grad_fixture(path)
+    grads = L.lattice_backward(*inputs, f["dy"], valid=valid, arch=str(f["arch"]))
+    for name, got in zip(GRAD_NAMES, grads):
+        error = scaled(got, f["d" + name])
+        assert error <= 2e-6, f"d{name}: scaled error {error:.3e}"
+
+
+def _finite_difference(inputs, dy, valid, arch, index, h=1e-6):
+    grad = np.zeros_like(inputs[index])
+    for position in np.ndindex(grad.shape):
+        values = []
+        for sign in (1.0, -1.0):
+            moved = [a.copy() for a in inputs]
+            moved[index][position] += sign * h
+            y, _ = L.lattice_scan_sequential(*moved, valid=valid, arch=arch, dtype=np.float64)
+            values.append(float((y * dy).sum()))
+        grad[position] = (values[0] - values[1]) / (2 * h)
+    return grad
+
+
+@pytest.mark.parametrize("arch,K,M", [("cauchy_x_hyperbolic", 2, 3), ("expsoftplus_x_mobius", 3, 2),
+                                      ("hill_x_identity", 1, 2), ("expexp_x_mobius", 2, 1),
+                                      ("gaussian_x_hyperbolic", 4, 1)])
+def test_backward_matches_finite_differences(arch, K, M):
+    """Central differences of the fp64 stage-loop forward, every element of every input."""
+    rng = np.random.default_rng(K * 10 + M)
+    inputs = [v.astype(np.float64) for v in L.random_inputs(rng, 2, 5, 3, K, M, scale=(0.5,) * 7)]
+    valid = rng.random((2, 5)) > 0.3
+    dy = rng.standard_normal((2, 5, 3))
+    grads = dict(zip(GRAD_NAMES, L.lattice_backward(*inputs, dy, valid=valid, arch=arch)))
+    for name, index in zip(("x", "alpha", "rho", "gamma", "write", "read", "beta"), range(7)):
+        want = _finite_difference(inputs, dy, valid, arch, index)
+        error = np.abs(grads[name] - want).max() / np.abs(want).max()
+        assert error <= 1e-7, f"d{name}: relative error {error:.3e}"
+
+
+def test_backward_planted_mistakes_fail(monkeypatch):
+    """A sign slip in a rotation derivative, or sigmoid in place of SiLU's derivative, misses
+    the reference's gradients by far more than the tolerance."""
+    f, inputs, valid = _grad_fixture(os.path.join(GOLDEN, "grad_k2m16_cauchy_x_mobius.npz"))
+    derivatives = L.stage_map_derivatives
+
+    def flipped(alpha, beta, arch):
+        cos, sin, r, dcos, dsin, dr = derivatives(alpha, beta, arch)
+        return cos, sin, r, dcos, -dsin, dr
+
+    monkeypatch.setattr(L, "stage_map_derivatives", flipped)
+    grads = L.lattice_backward(*inputs, f["dy"], valid=valid, arch="cauchy_x_mobius")
+    assert scaled(grads[1], f["dalpha"]) > 0.1
+    monkeypatch.undo()
+    monkeypatch.setattr(L, "silu_derivative", lambda g: 1.0 / (1.0 + np.exp(-g)))
+    grads = L.lattice_backward(*inputs, f["dy"], valid=valid, arch="cauchy_x_mobius")
+    assert scaled(grads[4], f["dgamma"]) > 0.01
