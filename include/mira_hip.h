@@ -73,6 +73,26 @@ int mira_lattice_forward(const void *x, int64_t x_row, const void *alpha, int64_
                          int K, int M, int dtype, int arch_mode, int chunk, void *workspace,
                          size_t workspace_bytes, void *stream);
 
+/* Allocation-free variant of mira_lattice_forward. It has no counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP-graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Arguments and results are mira_lattice_forward's
+ * without the workspace: the chunk summaries live in a static device array of
+ * MIRA_LATTICE_STATIC_SCRATCH_BYTES per GPU, which the library holds until the process ends; the
+ * call allocates nothing and clears nothing (every scratch word it reads it wrote first). A call
+ * whose chunk plan needs more than that (mira_lattice_workspace_bytes) returns MIRA_ERR_ARG;
+ * pass a longer chunk (chunk = T needs none) or use mira_lattice_forward. All calls on one GPU
+ * share the array, so calls that overlap in time on one GPU (two streams, two threads) race:
+ * the caller must order them. */
+#define MIRA_LATTICE_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+int mira_lattice_forward_static(const void *x, int64_t x_row, const void *alpha,
+                                int64_t alpha_row, const void *beta, int64_t beta_row,
+                                const void *rho, int64_t rho_row, const void *gamma,
+                                int64_t gamma_row, const void *memory_write,
+                                const void *memory_read, int64_t read_row, const uint8_t *valid,
+                                const float *state_in, float *state_out, void *out, int B, int T,
+                                int C, int K, int M, int dtype, int arch_mode, int chunk,
+                                void *stream);
+
 /* The decode step, T = 1: replaces mira_matrix_step_k{K}_m{M}_{dt}
  * (kernel/cuda/mira_dspv2/mira_iir.cu:376-411, launched at mira.py:1254-1276 when tokens == 1).
  * Same arguments as mira_lattice_forward at T = 1; no workspace. state_in and state_out may be

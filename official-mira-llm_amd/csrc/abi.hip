@@ -5,12 +5,38 @@
 #include "mira_abi_internal.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 namespace mira {
 
 namespace {
 thread_local std::string g_last_error;
+
+// The static scratch of mira_lattice_forward_static: one array per GPU (each device holds its
+// own copy at its own address), resolved once per device by hipGetSymbolAddress. Host code only
+// ever passes the resolved device address; the array's name is a host-side stand-in.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[MIRA_LATTICE_STATIC_SCRATCH_BYTES];
+std::mutex g_scratch_lock;
+void *g_scratch[kMaxDevices] = {};
+
+int static_scratch(void **address) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
+        return fail(MIRA_ERR_HIP, "mira: no current HIP device for the static scratch");
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (!g_scratch[device]) {
+        void *resolved = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&resolved, HIP_SYMBOL(scratch));
+        if (status != hipSuccess || !resolved)
+            return fail(MIRA_ERR_HIP, std::string("mira: hipGetSymbolAddress(scratch) failed: ") +
+                                          hipGetErrorString(status));
+        g_scratch[device] = resolved;
+    }
+    *address = g_scratch[device];
+    return MIRA_OK;
+}
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 }  // namespace
@@ -99,6 +125,42 @@ int mira_lattice_forward(const void *x, int64_t x_row, const void *alpha, int64_
             return fail(MIRA_ERR_ARG, "mira: workspace smaller than mira_lattice_workspace_bytes");
         const long long planes = (long long)B * a.chunks * C;
         a.phi = static_cast<float *>(workspace);
+        a.carry = a.phi + planes * K * K;
+    }
+    return lattice_launch(a, static_cast<hipStream_t>(stream));
+}
+
+int mira_lattice_forward_static(const void *x, int64_t x_row, const void *alpha,
+                                int64_t alpha_row, const void *beta, int64_t beta_row,
+                                const void *rho, int64_t rho_row, const void *gamma,
+                                int64_t gamma_row, const void *memory_write,
+                                const void *memory_read, int64_t read_row, const uint8_t *valid,
+                                const float *state_in, float *state_out, void *out, int B, int T,
+                                int C, int K, int M, int dtype, int arch_mode, int chunk,
+                                void *stream) {
+    LatticeArgs a{};
+    a.x = x; a.alpha = alpha; a.beta = beta; a.rho = rho; a.gamma = gamma;
+    a.write = memory_write; a.read = memory_read; a.valid = valid;
+    a.state_in = state_in; a.state_out = state_out; a.out = out;
+    a.B = B; a.T = T; a.C = C; a.K = K; a.M = M; a.dtype = dtype; a.mode = arch_mode;
+    if (int rc = lattice_common(a, x_row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+        return rc;
+    if (chunk <= 0) chunk = lattice_plan_chunk(B, T, C, K, M);
+    if (chunk > T) chunk = T;
+    a.chunk = chunk;
+    a.chunks = (T + chunk - 1) / chunk;
+    const size_t need = lattice_workspace(B, T, C, K, M, chunk);
+    if (need > MIRA_LATTICE_STATIC_SCRATCH_BYTES)
+        return fail(MIRA_ERR_ARG, "mira: this call's chunk summaries need " + std::to_string(need) +
+                                      " bytes, over the " +
+                                      std::to_string(MIRA_LATTICE_STATIC_SCRATCH_BYTES) +
+                                      "-byte static scratch; pass a longer chunk or use "
+                                      "mira_lattice_forward with a workspace");
+    if (need > 0) {
+        void *base = nullptr;
+        if (int rc = static_scratch(&base)) return rc;
+        const long long planes = (long long)B * a.chunks * C;
+        a.phi = static_cast<float *>(base);
         a.carry = a.phi + planes * K * K;
     }
     return lattice_launch(a, static_cast<hipStream_t>(stream));
