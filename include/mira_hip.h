@@ -93,6 +93,36 @@ int mira_lattice_forward_static(const void *x, int64_t x_row, const void *alpha,
                                 int C, int K, int M, int dtype, int arch_mode, int chunk,
                                 void *stream);
 
+/* The backward (training): gradients of sum(grad_out * y) for y = mira_lattice_forward(...) with
+ * respect to x, alpha, beta, rho, gamma, memory_write and memory_read. Replaces the b1 -> reverse
+ * tree -> b3 -> b4 launches of MatrixLatticeIIR.backward (kernel/cuda/mira_dspv2/mira.py:
+ * 1295-1433, backward.cuh) and the fine checkpoints its forward keeps (mira.py:1165-1170).
+ *
+ * The forward must have run with chunk = mira_lattice_backward_chunk(K, M) (0 when (K, M) has no
+ * backward: the reference's ORDER_MEMORIES, K in {1,8} with d_m in {8,16}, K in {2,4} with
+ * d_m in {8,16,32,64}); its workspace, which then holds every chunk's transition and the state
+ * entering it, is passed back as forward_workspace (may be NULL when T <= that chunk), together
+ * with the same inputs, valid mask and state_in. grad_out [B,T,C] is contiguous in x's dtype.
+ * Every gradient is written in x's dtype at its own row stride (so the caller may point them at
+ * views of packed projection gradients); with raw_write non-NULL ([B,T,M] at raw_write_row),
+ * grad_write receives the gradient of the raw write, d/dz of SiLU(z) applied. workspace: at least
+ * mira_lattice_backward_workspace_bytes(B,T,C,K,M) bytes. */
+int mira_lattice_backward_chunk(int K, int M);
+size_t mira_lattice_backward_workspace_bytes(int B, int T, int C, int K, int M);
+int mira_lattice_backward(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,
+                          const void *beta, int64_t beta_row, const void *rho, int64_t rho_row,
+                          const void *gamma, int64_t gamma_row, const void *memory_write,
+                          const void *memory_read, int64_t read_row, const uint8_t *valid,
+                          const float *state_in, const void *grad_out, void *grad_x,
+                          int64_t grad_x_row, void *grad_alpha, int64_t grad_alpha_row,
+                          void *grad_beta, int64_t grad_beta_row, void *grad_rho,
+                          int64_t grad_rho_row, void *grad_gamma, int64_t grad_gamma_row,
+                          void *grad_write, int64_t grad_write_row, const void *raw_write,
+                          int64_t raw_write_row, void *grad_read, int64_t grad_read_row, int B,
+                          int T, int C, int K, int M, int dtype, int arch_mode,
+                          const void *forward_workspace, size_t forward_workspace_bytes,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
 /* The decode step, T = 1: replaces mira_matrix_step_k{K}_m{M}_{dt}
  * (kernel/cuda/mira_dspv2/mira_iir.cu:376-411, launched at mira.py:1254-1276 when tokens == 1).
  * Same arguments as mira_lattice_forward at T = 1; no workspace. state_in and state_out may be

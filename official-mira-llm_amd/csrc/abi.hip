@@ -166,6 +166,76 @@ int mira_lattice_forward_static(const void *x, int64_t x_row, const void *alpha,
     return lattice_launch(a, static_cast<hipStream_t>(stream));
 }
 
+int mira_lattice_backward_chunk(int K, int M) { return lattice_backward_chunk(K, M); }
+
+size_t mira_lattice_backward_workspace_bytes(int B, int T, int C, int K, int M) {
+    if (B <= 0 || T <= 0 || C <= 0 || K <= 0 || M <= 0) return 0;
+    return lattice_backward_workspace(B, T, C, K, M);
+}
+
+int mira_lattice_backward(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,
+                          const void *beta, int64_t beta_row, const void *rho, int64_t rho_row,
+                          const void *gamma, int64_t gamma_row, const void *memory_write,
+                          const void *memory_read, int64_t read_row, const uint8_t *valid,
+                          const float *state_in, const void *grad_out, void *grad_x,
+                          int64_t grad_x_row, void *grad_alpha, int64_t grad_alpha_row,
+                          void *grad_beta, int64_t grad_beta_row, void *grad_rho,
+                          int64_t grad_rho_row, void *grad_gamma, int64_t grad_gamma_row,
+                          void *grad_write, int64_t grad_write_row, const void *raw_write,
+                          int64_t raw_write_row, void *grad_read, int64_t grad_read_row, int B,
+                          int T, int C, int K, int M, int dtype, int arch_mode,
+                          const void *forward_workspace, size_t forward_workspace_bytes,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+    LatticeArgs f{};
+    f.x = x; f.alpha = alpha; f.beta = beta; f.rho = rho; f.gamma = gamma;
+    f.write = memory_write; f.read = memory_read; f.out = const_cast<void *>(grad_out);
+    f.B = B; f.T = T; f.C = C; f.K = K; f.M = M; f.dtype = dtype; f.mode = arch_mode;
+    if (int rc = lattice_common(f, x_row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+        return rc;
+    const int chunk = lattice_backward_chunk(K, M);
+    if (!chunk)
+        return fail(MIRA_DECLINE, "mira: no backward kernel for K=" + std::to_string(K) +
+                                      " d_m=" + std::to_string(M));
+    if (!grad_x || !grad_alpha || !grad_beta || !grad_rho || !grad_gamma || !grad_write ||
+        !grad_read)
+        return fail(MIRA_ERR_ARG, "mira: a gradient output is null");
+    if (grad_x_row < C || grad_gamma_row < C || grad_alpha_row < (int64_t)C * K ||
+        grad_beta_row < (int64_t)C * K || grad_rho_row < (int64_t)C * (K + 1) ||
+        grad_write_row < M || grad_read_row < (int64_t)(K + 1) * M ||
+        (raw_write && raw_write_row < M))
+        return fail(MIRA_ERR_ARG, "mira: a gradient row stride is narrower than its row");
+    LatticeBackArgs a{};
+    a.x = x; a.x_row = x_row; a.alpha = alpha; a.alpha_row = alpha_row; a.beta = beta;
+    a.beta_row = beta_row; a.rho = rho; a.rho_row = rho_row; a.gamma = gamma;
+    a.gamma_row = gamma_row; a.write = memory_write; a.read = memory_read; a.read_row = read_row;
+    a.valid = valid; a.state_in = state_in; a.grad_out = grad_out;
+    a.grad_x = grad_x; a.grad_x_row = grad_x_row; a.grad_alpha = grad_alpha;
+    a.grad_alpha_row = grad_alpha_row; a.grad_beta = grad_beta; a.grad_beta_row = grad_beta_row;
+    a.grad_rho = grad_rho; a.grad_rho_row = grad_rho_row; a.grad_gamma = grad_gamma;
+    a.grad_gamma_row = grad_gamma_row; a.grad_write = grad_write;
+    a.grad_write_row = grad_write_row; a.raw_write = raw_write; a.raw_write_row = raw_write_row;
+    a.grad_read = grad_read; a.grad_read_row = grad_read_row;
+    a.B = B; a.T = T; a.C = C; a.K = K; a.M = M; a.dtype = dtype; a.mode = arch_mode;
+    a.chunk = chunk;
+    a.chunks = (T + chunk - 1) / chunk;
+    if (a.chunks > 1) {
+        const size_t need = lattice_workspace(B, T, C, K, M, chunk);
+        if (!forward_workspace || forward_workspace_bytes < need)
+            return fail(MIRA_ERR_ARG, "mira: the backward needs the workspace of a forward run at "
+                                      "mira_lattice_backward_chunk's chunk length");
+        const long long planes = (long long)B * a.chunks * C;
+        a.phi = static_cast<const float *>(forward_workspace);
+        a.entering = a.phi + planes * K * K;
+    }
+    const size_t need = lattice_backward_workspace(B, T, C, K, M);
+    if (!workspace || workspace_bytes < need)
+        return fail(MIRA_ERR_ARG, "mira: workspace smaller than mira_lattice_backward_workspace_bytes");
+    float *base = static_cast<float *>(workspace);
+    a.adjoint = a.chunks > 1 ? base : nullptr;
+    a.partial = base + (a.chunks > 1 ? (long long)B * a.chunks * C * K * M : 0);
+    return lattice_backward_launch(a, static_cast<hipStream_t>(stream));
+}
+
 int mira_lattice_step(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,
                       const void *beta, int64_t beta_row, const void *rho, int64_t rho_row,
                       const void *gamma, int64_t gamma_row, const void *memory_write,

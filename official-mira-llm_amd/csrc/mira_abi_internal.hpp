@@ -40,6 +40,37 @@ int lattice_plan_chunk(int B, int T, int C, int K, int M);
 size_t lattice_workspace(int B, int T, int C, int K, int M, int chunk);
 int lattice_launch(LatticeArgs &a, hipStream_t stream);
 
+// --- the lattice backward (gradients of the scan) --------------------------------------------
+struct LatticeBackArgs {
+    const void *x;       long long x_row;
+    const void *alpha;   long long alpha_row;
+    const void *beta;    long long beta_row;
+    const void *rho;     long long rho_row;
+    const void *gamma;   long long gamma_row;
+    const void *write;                         // [B,T,M] contiguous
+    const void *read;    long long read_row;   // [B,T,K+1,M], dense tail
+    const uint8_t *valid;                      // [B,T] or null
+    const float *state_in;                     // [B,K,C,M] or null (the forward's entering state)
+    const void *grad_out;                      // [B,T,C] contiguous
+    void *grad_x;        long long grad_x_row;
+    void *grad_alpha;    long long grad_alpha_row;
+    void *grad_beta;     long long grad_beta_row;
+    void *grad_rho;      long long grad_rho_row;
+    void *grad_gamma;    long long grad_gamma_row;
+    void *grad_write;    long long grad_write_row;
+    const void *raw_write; long long raw_write_row;   // or null: grad_write gets SiLU' of it
+    void *grad_read;     long long grad_read_row;
+    int B, T, C, K, M, dtype, mode;
+    int chunk, chunks, groups;
+    const float *phi;                          // forward workspace: [B,chunks,C,K,K]
+    const float *entering;                     // forward workspace: [B,chunks,C,K,M]
+    float *adjoint;                            // [B,chunks,C,K,M]
+    float *partial;                            // [groups,B,T,K+2,M]
+};
+int lattice_backward_chunk(int K, int M);
+size_t lattice_backward_workspace(int B, int T, int C, int K, int M);
+int lattice_backward_launch(LatticeBackArgs &a, hipStream_t stream);
+
 // --- the lattice scan forming its coefficients from the control ------------------------------
 struct LatticeControlArgs {
     const void *x;        long long x_row;

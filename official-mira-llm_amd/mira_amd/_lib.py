@@ -35,6 +35,11 @@ SIGNATURES = {
                               i32, i32, i32, i32, i32, i32, i32, i32, p, sz, p], i32),
     "mira_lattice_forward_static": ([p, i64, p, i64, p, i64, p, i64, p, i64, p, p, i64, p, p, p,
                                      p, i32, i32, i32, i32, i32, i32, i32, i32, p], i32),
+    "mira_lattice_backward_chunk": ([i32, i32], i32),
+    "mira_lattice_backward_workspace_bytes": ([i32, i32, i32, i32, i32], sz),
+    "mira_lattice_backward": ([p, i64, p, i64, p, i64, p, i64, p, i64, p, p, i64, p, p, p,
+                               p, i64, p, i64, p, i64, p, i64, p, i64, p, i64, p, i64, p, i64,
+                               i32, i32, i32, i32, i32, i32, i32, p, sz, p, sz, p], i32),
     "mira_lattice_step": ([p, i64, p, i64, p, i64, p, i64, p, i64, p, p, i64, p, p, p, p,
                            i32, i32, i32, i32, i32, i32, p], i32),
     "mira_lattice_control_serves": ([i32, i32, i32, i32, i32, i32, i32], i32),

@@ -21,8 +21,10 @@ plus the BASELINE-literal scans, which have no reference counterpart:
 
 A call the kernels do not serve returns None, exactly as the reference plugin does, and the
 mixer raises; a malformed state or mask raises ValueError; a failed launch raises RuntimeError.
-Every launch is asynchronous on torch's current stream of the tensors' device. The backward
-(training) pass is not built: a call that would need one declines.
+Every launch is asynchronous on torch's current stream of the tensors' device. A call under
+autograd without return_state keeps a graph (the _LatticeScan Function: the forward at the
+backward's chunk length, mira_lattice_backward in the backward, gradients written into the
+packed projections when the mixer passes them); a (K, d_m) without backward kernels declines.
 """
 from __future__ import annotations
 
@@ -176,8 +178,7 @@ def matrix_lattice_iir(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, 
         return None
     if len({tensor.device for tensor in tensors}) != 1 or len({t.dtype for t in tensors}) != 1:
         return None
-    dtype = DTYPE.get(x.dtype)
-    if dtype is None or not memory_write.is_contiguous():
+    if DTYPE.get(x.dtype) is None or not memory_write.is_contiguous():
         return None
     if not (raw_beta is not None and raw_beta.shape == raw_alpha.shape
             and raw_beta.dtype == raw_alpha.dtype and raw_beta.device == x.device):
@@ -194,8 +195,6 @@ def matrix_lattice_iir(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, 
         return None
     if not status(x.device.index)[0]:
         return None
-    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors + (raw_beta,)):
-        return None                          # a gradient needs the backward, which is not built
     if valid is not None:
         if valid.shape != (batch, tokens) or valid.device != x.device or valid.dtype != torch.bool:
             raise ValueError("mira-dsp mask must be a boolean [batch, tokens] CUDA tensor")
@@ -210,7 +209,69 @@ def matrix_lattice_iir(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, 
             raise ValueError("mira-dsp initial state requires return_state=True")
         state = state.contiguous()
     if packed is not None:
-        return None                          # packed projections exist for the backward only
+        _check_packed(packed, x, raw_alpha, raw_beta, raw_rho, memory_read, row,
+                      (alpha_row, beta_row, rho_row, read_row))
+    # a retained graph (gradients wanted, no state handed back) runs the training path; with
+    # return_state the scan serves a cache and carries no gradient (mira.py:1518-1563)
+    train = (not return_state and torch.is_grad_enabled() and any(
+        t.requires_grad for t in tensors + (raw_beta,) + (() if packed is None else tuple(packed))))
+    if train:
+        lib = _lib.require()
+        if not lib.mira_lattice_backward_chunk(order, memory):
+            return None                      # no backward kernel for this (K, d_m)
+        rows = (row, alpha_row, beta_row, rho_row, gamma_row, read_row)
+        if packed is not None:
+            x, raw_alpha, raw_beta, raw_rho, memory_write, memory_read = (
+                t.detach() for t in (x, raw_alpha, raw_beta, raw_rho, memory_write, memory_read))
+            packed_input, packed_coefficients = packed
+        else:
+            packed_input = packed_coefficients = None
+        output = _LatticeScan.apply(x, raw_alpha, raw_beta, raw_rho, gamma, memory_write,
+                                    memory_read, packed_input, packed_coefficients, valid, rows,
+                                    arch)
+        USED["forward"] += 1
+        return output
+    if return_state:
+        with torch.no_grad():
+            return _lattice_inference(x, raw_alpha, raw_beta, raw_rho, gamma, memory_write,
+                                      memory_read, valid, state, True, arch, chunk,
+                                      (row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+    return _lattice_inference(x, raw_alpha, raw_beta, raw_rho, gamma, memory_write, memory_read,
+                              valid, state, False, arch, chunk,
+                              (row, alpha_row, beta_row, rho_row, gamma_row, read_row))
+
+
+def _check_packed(packed, x, raw_alpha, raw_beta, raw_rho, memory_read, row, coefficient_rows):
+    """The packed projections of a training forward must be the storage the views come from
+    (mira.py:1518-1537): [B,T,C+M] input projection with x at its start, and the
+    [B,T,C(3K+1)+(K+1)M] coefficient projection holding alpha, beta, rho and nu in that order."""
+    batch, tokens, channels = x.shape
+    order = int(raw_alpha.shape[-1])
+    memory = int(memory_read.shape[-1])
+    packed_input, packed_coefficients = packed
+    width = channels * (3 * order + 1) + (order + 1) * memory
+    if (packed_input.shape != (batch, tokens, channels + memory)
+            or packed_coefficients.shape != (batch, tokens, width)
+            or not packed_input.is_contiguous() or not packed_coefficients.is_contiguous()
+            or any(t.device != x.device or t.dtype != x.dtype for t in packed)):
+        raise ValueError("mira-dsp packed projections have incompatible layout")
+    base, element = packed_coefficients.data_ptr(), x.element_size()
+    if (x.data_ptr() != packed_input.data_ptr() or raw_alpha.data_ptr() != base
+            or raw_beta.data_ptr() != base + channels * order * element
+            or raw_rho.data_ptr() != base + 2 * channels * order * element
+            or memory_read.data_ptr() != base + channels * (3 * order + 1) * element
+            or row != channels + memory or any(r != width for r in coefficient_rows)):
+        raise ValueError("mira-dsp packed views do not match their projection storage")
+
+
+def _lattice_inference(x, raw_alpha, raw_beta, raw_rho, gamma, memory_write, memory_read, valid,
+                       state, return_state, arch, chunk, rows):
+    """The forward without a retained graph: summary / combine / replay, or one launch."""
+    row, alpha_row, beta_row, rho_row, gamma_row, read_row = rows
+    batch, tokens, channels = x.shape
+    order = int(raw_alpha.shape[-1])
+    memory = int(memory_write.shape[-1])
+    dtype = DTYPE[x.dtype]
     lib = _lib.require()
     output = torch.empty(batch, tokens, channels, device=x.device, dtype=x.dtype)
     final = (torch.empty(batch, order, channels, memory, device=x.device, dtype=torch.float32)
@@ -231,6 +292,99 @@ def matrix_lattice_iir(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, 
         return None
     USED["forward"] += 1
     return (output, final) if return_state else output
+
+
+class _LatticeScan(torch.autograd.Function):
+    """The scan with a retained graph: the forward runs at the backward's chunk length and keeps
+    its workspace (every chunk's transition and entering state: the checkpoints the backward
+    replays from, mira.py:1165-1170); the backward launches mira_lattice_backward
+    (mira.py:1295-1433). With packed projections the gradients land in two packed buffers, the
+    raw write's through SiLU', and flow to the projections that made them."""
+
+    @staticmethod
+    def forward(ctx, x, raw_alpha, raw_beta, raw_rho, gamma, memory_write, memory_read,
+                packed_input, packed_coefficients, valid, rows, arch):
+        row, alpha_row, beta_row, rho_row, gamma_row, read_row = rows
+        batch, tokens, channels = x.shape
+        order, memory = int(raw_alpha.shape[-1]), int(memory_write.shape[-1])
+        lib = _lib.require()
+        chunk = lib.mira_lattice_backward_chunk(order, memory)
+        output = torch.empty(batch, tokens, channels, device=x.device, dtype=x.dtype)
+        need = lib.mira_lattice_workspace_bytes(batch, tokens, channels, order, memory, chunk)
+        space = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        with torch.cuda.device(x.device):
+            code = lib.mira_lattice_forward(
+                _ptr(x), row, _ptr(raw_alpha), alpha_row, _ptr(raw_beta), beta_row,
+                _ptr(raw_rho), rho_row, _ptr(gamma), gamma_row, _ptr(memory_write),
+                _ptr(memory_read), read_row, _ptr(valid), None, None, _ptr(output), batch,
+                tokens, channels, order, memory, DTYPE[x.dtype], ARCH_STAGE[arch], chunk,
+                _ptr(space), need, _stream(x.device))
+        _lib.check(code, "mira_lattice_forward")
+        ctx.save_for_backward(x, raw_alpha, raw_beta, raw_rho, gamma, memory_write, memory_read,
+                              space, valid, packed_input)
+        ctx.meta = (rows, arch, need, packed_coefficients is not None)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (x, raw_alpha, raw_beta, raw_rho, gamma, memory_write, memory_read, space, valid,
+         packed_input) = ctx.saved_tensors
+        rows, arch, forward_bytes, packed = ctx.meta
+        row, alpha_row, beta_row, rho_row, gamma_row, read_row = rows
+        batch, tokens, channels = x.shape
+        order, memory = int(raw_alpha.shape[-1]), int(memory_write.shape[-1])
+        grad_output = grad_output.to(x.dtype).contiguous()
+        io = dict(device=x.device, dtype=x.dtype)
+        if packed:
+            width = channels * (3 * order + 1) + (order + 1) * memory
+            grad_input = torch.empty(batch, tokens, channels + memory, **io)
+            grad_coefficients = torch.empty(batch, tokens, width, **io)
+            element = x.element_size()
+            base = grad_coefficients.data_ptr()
+            pointers = (grad_input.data_ptr(), channels + memory,
+                        base, width, base + channels * order * element, width,
+                        base + 2 * channels * order * element, width)
+            write_pointer = grad_input.data_ptr() + channels * element
+            read_pointer = base + channels * (3 * order + 1) * element
+            write_rows, read_rows = channels + memory, width
+            raw_write = packed_input.data_ptr() + channels * element
+            raw_rows = channels + memory
+        else:
+            grad_input = grad_coefficients = None
+            grads = [torch.empty(batch, tokens, channels, **io),
+                     torch.empty(batch, tokens, channels, order, **io),
+                     torch.empty(batch, tokens, channels, order, **io),
+                     torch.empty(batch, tokens, channels, order + 1, **io),
+                     torch.empty(batch, tokens, memory, **io),
+                     torch.empty(batch, tokens, order + 1, memory, **io)]
+            pointers = (grads[0].data_ptr(), channels, grads[1].data_ptr(), channels * order,
+                        grads[2].data_ptr(), channels * order, grads[3].data_ptr(),
+                        channels * (order + 1))
+            write_pointer, read_pointer = grads[4].data_ptr(), grads[5].data_ptr()
+            write_rows, read_rows = memory, (order + 1) * memory
+            raw_write, raw_rows = None, 0
+        grad_gamma = torch.empty(batch, tokens, channels, **io)
+        lib = _lib.require()
+        need = lib.mira_lattice_backward_workspace_bytes(batch, tokens, channels, order, memory)
+        scratch = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        with torch.cuda.device(x.device):
+            code = lib.mira_lattice_backward(
+                _ptr(x), row, _ptr(raw_alpha), alpha_row, _ptr(raw_beta), beta_row,
+                _ptr(raw_rho), rho_row, _ptr(gamma), gamma_row, _ptr(memory_write),
+                _ptr(memory_read), read_row, _ptr(valid), None, _ptr(grad_output),
+                pointers[0], pointers[1], pointers[2], pointers[3], pointers[4], pointers[5],
+                pointers[6], pointers[7], _ptr(grad_gamma), channels, write_pointer, write_rows,
+                raw_write, raw_rows, read_pointer, read_rows, batch, tokens, channels, order,
+                memory, DTYPE[x.dtype], ARCH_STAGE[arch], _ptr(space), forward_bytes,
+                _ptr(scratch), need, _stream(x.device))
+        _lib.check(code, "mira_lattice_backward")
+        USED["backward"] += 1
+        if packed:
+            return (None, None, None, None, grad_gamma, None, None, grad_input, grad_coefficients,
+                    None, None, None)
+        wanted = ctx.needs_input_grad
+        values = (grads[0], grads[1], grads[2], grads[3], grad_gamma, grads[4], grads[5])
+        return tuple(v if wanted[i] else None for i, v in enumerate(values)) + (None,) * 5
 
 
 def matrix_lattice_step(x, raw_alpha, raw_rho, gamma, memory_write, memory_read, raw_beta,

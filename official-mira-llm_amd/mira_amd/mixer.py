@@ -6,10 +6,12 @@ to_control d -> d_r, to_gate d -> d_e, coefficient_projection d_r -> alpha | bet
 (d_e K + d_e K + d_e (K+1) + (K+1) d_m), out_proj d_e -> d (no bias). The forward projects,
 splits the fused projections into strided views (no copies, model/mira_mixer.py:807-813), takes
 s = SiLU(raw write), and hands everything to mira_amd.mira.matrix_lattice_iir with the prefix
-cache's state. An uncached, gradient-free forward hands the scan the d_r-wide control and
-coefficient_projection instead (mira_amd.mira.matrix_lattice_iir_control, which forms alpha, beta
-and rho inside the scan where it can; model/mira_mixer.py:739-760). There is no PyTorch fallback:
-a declined call raises, as in the reference (model/mira_mixer.py:822-824).
+cache's state; with gradients it also hands over the two projection outputs those views come
+from, so the plugin's backward writes into them whole. An uncached, gradient-free forward hands
+the scan the d_r-wide control and coefficient_projection instead
+(mira_amd.mira.matrix_lattice_iir_control, which forms alpha, beta and rho inside the scan where
+it can; model/mira_mixer.py:739-760). There is no PyTorch fallback: a declined call raises, as in
+the reference (model/mira_mixer.py:822-824).
 
 The reference's lattice initializer (model/mira_initializer.py, Jeffreys-prior pole placement)
 is out of scope here; parameters use torch's default nn.Linear initialisation.
@@ -155,11 +157,6 @@ class MiraMixer(nn.Module):
         if cache is not None and not (prefix_cache.enabled() and layer is not None
                                       and not self.training and hasattr(cache, "get")):
             raise ValueError("streaming cache is not wired into mira-dsp")
-        if torch.is_grad_enabled() and (normalized_x.requires_grad or any(
-                p.requires_grad for p in self.parameters())):
-            raise RuntimeError("the MI355X mixer serves inference only (the lattice scan has no "
-                               "backward here): run it under torch.no_grad() or "
-                               "torch.inference_mode(), or freeze its parameters")
         batch, tokens, _ = normalized_x.shape
         channels, order, memory = self.inner, self.order, self.memory_dimension
         if self._forms_coefficients_in_scan(normalized_x, cache):
@@ -189,6 +186,11 @@ class MiraMixer(nn.Module):
             value = raw_alpha.float()
             safe = torch.where(value == 0.0, torch.full_like(value, 1.0e-6), value)
             raw_alpha = torch.where(value.abs() < 1.0, safe.reciprocal(), value).to(raw_alpha.dtype)
+            if torch.is_grad_enabled() and cache is None:
+                # the remapped alpha must live in the packed storage the backward writes into
+                coefficients = torch.cat((raw_alpha, raw_beta, raw_rho, memory_read), dim=-1)
+                raw_alpha, raw_beta, raw_rho, memory_read = coefficients.split(
+                    (alpha_size, alpha_size, rho_size, read_size), dim=-1)
         memory_write = F.silu(raw_write)
         raw_alpha = raw_alpha.view(batch, tokens, channels, order)
         raw_beta = raw_beta.view(batch, tokens, channels, order)
@@ -204,10 +206,14 @@ class MiraMixer(nn.Module):
                 raw_beta, held, valid=valid, arch=self.arch,
                 inplace=bool(getattr(cache, "in_place", False)))
         else:
+            # training hands the plugin the two projection outputs the views come from, so the
+            # backward writes its gradients into them whole (model/mira_mixer.py:814-821)
+            packed = ((input_projection, coefficients)
+                      if torch.is_grad_enabled() and cache is None else None)
             result = plugin.matrix_lattice_iir(
                 signal, raw_alpha, raw_rho, gamma, memory_write.contiguous(), memory_read,
                 raw_beta=raw_beta, valid=valid, state=held,
-                return_state=cache is not None, arch=self.arch)
+                return_state=cache is not None, packed=packed, arch=self.arch)
         if result is None:
             raise RuntimeError(_declined(signal, order, memory))
         if cache is None:

@@ -121,3 +121,35 @@ def test_control_scan_plan_and_errors(lib):
     assert call(order=8) == 1
     assert call(alpha_first=-1) == 2
     assert call(weight_rows=2 * C * K) == 2 and b"outside the weight" in lib.mira_last_error()
+
+
+def test_backward_plan_and_errors(lib):
+    """mira_lattice_backward_chunk: the chunk a training forward runs at (<= 16 tokens so a lane
+    holds the chunk's states), 0 where (K, d_m) has no backward (the reference's ORDER_MEMORIES:
+    K 1 and 8 at d_m 8, 16; K 2 and 4 at d_m 8..64); argument errors before any launch."""
+    assert lib.mira_lattice_backward_chunk(2, 16) == 16
+    assert lib.mira_lattice_backward_chunk(2, 64) == 16
+    assert lib.mira_lattice_backward_chunk(1, 8) == 4
+    for K, M in ((2, 128), (1, 32), (8, 32), (2, 1), (3, 16)):
+        assert lib.mira_lattice_backward_chunk(K, M) == 0, (K, M)
+    assert lib.mira_lattice_backward_workspace_bytes(2, 100, 64, 2, 16) > 0
+    assert lib.mira_lattice_backward_workspace_bytes(2, 100, 64, 2, 128) == 0
+    fake, null = ctypes.c_void_p(256), None
+    args = [fake, 64, fake, 128, fake, 128, fake, 192, fake, 64, fake, fake, 48, null, null, fake]
+    grads = [fake, 64, fake, 128, fake, 128, fake, 192, fake, 64, fake, 16, null, 0, fake, 48]
+    tail = [2, 100, 64, 2, 16, 0, 6]
+    # a missing gradient output: bad argument
+    bad = list(grads)
+    bad[4] = null
+    assert lib.mira_lattice_backward(*args, *bad, *tail, fake, 1 << 30, fake, 1 << 30, null) == 2
+    # no forward workspace over several chunks: bad argument
+    assert lib.mira_lattice_backward(*args, *grads, *tail, null, 0, fake, 1 << 30, null) == 2
+    assert b"forward" in lib.mira_last_error()
+    # a (K, d_m) without backward kernels declines
+    tail_wide = [2, 100, 64, 2, 128, 0, 6]
+    wide_args = list(args)
+    wide_args[12] = 3 * 128
+    wide_grads = list(grads)
+    wide_grads[11], wide_grads[15] = 128, 3 * 128
+    assert lib.mira_lattice_backward(*wide_args, *wide_grads, *tail_wide, fake, 1 << 30, fake,
+                                     1 << 30, null) == 1

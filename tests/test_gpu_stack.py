@@ -164,10 +164,11 @@ def test_rms_norm_against_the_stepwise_form(torch_mod, dtype):
         assert bool((gap <= ulp).all()), f"width {width}: a gap over one bf16 ulp"
 
 
-def test_gradients_are_refused_not_dropped(torch_mod, model_cls):
-    """There is no backward for the scan: under autograd the plugin declines (even with a state,
-    where the reference would return one with a gradient) and the mixer raises, instead of
-    returning values that carry no gradient."""
+def test_gradient_rules(torch_mod, model_cls):
+    """Under autograd the scan keeps a graph only where the reference's does: with return_state
+    (a cache) it runs without one and hands back outputs that carry no gradient
+    (kernel/cuda/mira_dspv2/mira.py:1538-1563); a (K, d_m) without backward kernels declines
+    (None, and the mixer raises) instead of dropping the gradient; a served one trains."""
     torch = torch_mod
     from mira_amd import mira
     from oracle import lattice as L
@@ -176,11 +177,16 @@ def test_gradients_are_refused_not_dropped(torch_mod, model_cls):
     values = [torch.tensor(v, device="cuda").requires_grad_() for v in L.random_inputs(rng, 1, 5, 8, 2, 16)]
     x, alpha, rho, gamma, write, read, beta = values
     state = torch.zeros(1, 2, 8, 16, device="cuda")
-    assert mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta, state=state,
-                                   return_state=True) is None
+    y, final = mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta,
+                                       state=state, return_state=True)
+    assert not y.requires_grad and not final.requires_grad
+    assert mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta).requires_grad
+    wide = [torch.tensor(v, device="cuda").requires_grad_()
+            for v in L.random_inputs(rng, 1, 5, 8, 2, 128)]
+    assert mira.matrix_lattice_iir(*wide[:6], raw_beta=wide[6]) is None
+    with torch.no_grad():
+        assert mira.matrix_lattice_iir(*wide[:6], raw_beta=wide[6]) is not None
     model = _model(torch, model_cls, 3, torch.float32)
     ids = torch.tensor([[1, 2, 3]], device="cuda")
-    with pytest.raises(RuntimeError, match="inference only"):
-        model(ids)
-    with torch.no_grad():
-        assert model(ids).logits.shape == (1, 3, CFG["vocab_size"])
+    model(ids).logits.sum().backward()
+    assert model.blocks[0].mixer.coefficient_projection.weight.grad is not None
