@@ -1,6 +1,7 @@
 """Benchmark of the Mira mixer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-stack] [--no-traffic]
+                    [--only LEG ...]
 
 Headline (BASELINE.json `metric`, `configs[1]`): bf16 prefill of the depthwise causal conv
 (width 4) + diagonal decay scan at B=8, T=4096, D=2048 with a carried-in fp32 state, inputs
@@ -12,8 +13,12 @@ sample of the same workload. Also reported, not headline: the GLA chunked prefil
 % HBM and % MFMA), the reference operator matrix_lattice_iir at the cfg5 mixer geometry
 (K=2, M=64), matrix_lattice_iir_control (coefficients formed inside the scan) at the
 reference's own mixer geometry against its materialised path, and the 24-layer MiraLLM forward
-of `configs[4]` with the mixer's and the scan's share of its time (skip it with --no-stack).
-Prints one JSON line.
+of `configs[4]` with the mixer's and the scan's share of its time (skip it with --no-stack), and a
+training step of the scan (forward + backward) at the reference's mira-s and the cfg5 geometry.
+The headline kernel's HBM traffic is measured in the same run by two rocprofv3 --pmc child runs
+(FETCH_SIZE, WRITE_SIZE) started before this process initialises the GPU (skip with
+--no-traffic). `--only LEG` runs the headline plus the named legs (`--only prefill`: the headline
+alone), which is how each kernel is profiled on its own. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -28,6 +33,10 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "official-mira-llm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+LEGS = ("decode", "gla", "lattice", "control", "backward", "stack")
+ONLY = ("prefill",) + LEGS
+CALIBRATION_KERNEL = "neg_kernel"                 # torch.neg over 64 Mi bf16 elements:
+CALIBRATION_KIB = 131072.0                         # it reads 128 MiB and writes 128 MiB
 METRIC = "prefill scan tokens/s + % HBM roofline; decode steps/s at batch 256"
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -42,22 +51,20 @@ def parse():
                         help="skip the 24-layer MiraLLM forward (BASELINE configs[4])")
     parser.add_argument("--decode-steps", type=int, default=128)
     parser.add_argument("--calibrate", action="store_true",
-                        help="also run an elementwise kernel of known traffic (reads and writes "
-                             "128 MiB each) five times, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE")
+                        help="also run an elementwise kernel of known traffic (torch.neg: reads "
+                             "and writes 128 MiB each) five times, to scale rocprofv3 FETCH_SIZE / "
+                             "WRITE_SIZE")
+    parser.add_argument("--only", action="append", choices=ONLY, default=None,
+                        help="run only these legs (repeatable), e.g. to profile one kernel; the "
+                             "headline prefill leg always runs")
+    parser.add_argument("--no-traffic", action="store_true",
+                        help="skip the live rocprofv3 FETCH_SIZE / WRITE_SIZE runs of the headline "
+                             "kernel")
+    parser.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     return parser.parse_args()
 
 
-def traffic_from_profiles(kernel):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
-    copy-kernel calibration), when a summary for this kernel is committed under profiles/."""
-    path = os.path.join(PROFILES, f"{kernel}_traffic.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as handle:
-        return json.load(handle).get("bytes_per_launch")
-
-
-def prefill_leg(torch, mira, steps, warmup):
+def _prefill_inputs(torch):
     B, T, D = 8, 4096, 2048
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(B, T, D, device="cuda", generator=g).to(torch.bfloat16)
@@ -65,6 +72,82 @@ def prefill_leg(torch, mira, steps, warmup):
     w = torch.randn(D, 4, device="cuda", generator=g) * 0.5
     bias = torch.zeros(D, device="cuda")
     h0 = torch.randn(B, D, device="cuda", generator=g) * 0.1
+    return (B, T, D), (x, a, w, bias, h0)
+
+
+def traffic_child():
+    """What the traffic measurement profiles: the calibration copy (torch.neg over 64 Mi bf16
+    elements: 128 MiB read, 128 MiB written; no other kernel of this process is a neg) and the
+    headline prefill kernel, three times each."""
+    import torch
+
+    from mira_amd import mira
+
+    _, (x, a, w, bias, h0) = _prefill_inputs(torch)
+    calibrate(torch, 3)
+    for _ in range(3):
+        mira.diag_conv_scan(x, a, w, bias, h0=h0, return_state=True)
+    torch.cuda.synchronize()
+
+
+def calibrate(torch, times):
+    """The copy of known traffic that scales rocprofv3's FETCH_SIZE and WRITE_SIZE readings."""
+    source = torch.ones(64 << 20, device="cuda", dtype=torch.bfloat16)
+    target = torch.empty_like(source)
+    for _ in range(times):
+        torch.neg(source, out=target)
+    torch.cuda.synchronize()
+
+
+def measure_traffic(kernel="diag_column_kernel"):
+    """HBM bytes per launch of the headline kernel in this run: two rocprofv3 --pmc child runs of
+    `bench.py --traffic-child` (FETCH_SIZE, then WRITE_SIZE: one TCC counter set per run), each
+    counter scaled by what it reads for the calibration copy of known size. Run before this
+    process touches the GPU. Returns (dict or None, reason)."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    profiler = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(profiler):
+        return None, "rocprofv3 not found"
+    measured = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix=f"mira_{counter.lower()}_", dir="/tmp")
+        command = [profiler, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "t",
+                   "--", sys.executable, os.path.abspath(__file__), "--traffic-child"]
+        try:
+            subprocess.run(command, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
+                           stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=150,
+                           check=False)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 --pmc {counter} did not finish in 150 s"
+        rows = []
+        for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as handle:
+                rows += list(csv.DictReader(handle))
+        shutil.rmtree(out, ignore_errors=True)
+        values = {"kernel": [], "calibration": []}
+        for row in rows:
+            name = row.get("Kernel_Name", "")
+            if kernel in name:
+                values["kernel"].append(float(row["Counter_Value"]))
+            elif CALIBRATION_KERNEL in name:
+                values["calibration"].append(float(row["Counter_Value"]))
+        if not values["kernel"] or not values["calibration"]:
+            return None, f"rocprofv3 --pmc {counter} returned no rows for the kernel or the copy"
+        scale = CALIBRATION_KIB / (sum(values["calibration"]) / len(values["calibration"]))
+        measured[counter] = (sum(values["kernel"]) / len(values["kernel"]) * scale * 1024, scale)
+    fetch, write = measured["FETCH_SIZE"], measured["WRITE_SIZE"]
+    return {"bytes": round(fetch[0] + write[0]), "fetch_bytes": round(fetch[0]),
+            "write_bytes": round(write[0]), "fetch_scale": round(fetch[1], 4),
+            "write_scale": round(write[1], 4)}, ""
+
+
+def prefill_leg(torch, mira, steps, warmup):
+    (B, T, D), (x, a, w, bias, h0) = _prefill_inputs(torch)
     for _ in range(warmup):
         mira.diag_conv_scan(x, a, w, bias, h0=h0, return_state=True)
     # one launch per step, back to back on the launch stream; HIP events around the timed
@@ -329,6 +412,57 @@ def control_leg(torch, mira, steps, warmup):
             "identical": same, "shape": f"B={B} T={T} C={C} K={K} M={M} d_r={R}"}
 
 
+def backward_leg(torch, mira, steps, warmup):
+    """A training step of the scan: matrix_lattice_iir under autograd (the forward at the
+    backward's chunk length, keeping every chunk's entering state) and its backward (all seven
+    gradients: mira_lattice_backward), bf16 in/out, fp32 arithmetic, zero initial state, at the
+    reference's mira-s mixer geometry (d_e 1536, K 2, d_m 16) over B=8 T=2048 and at the cfg5
+    geometry (d_e 2048, K 2, d_m 64, B=4 T=2048). Times the forward alone and forward + backward
+    with HIP events on the launch stream."""
+    results = {}
+    bf = torch.bfloat16
+    for label, (B, T, C, K, M) in (("mira_s", (8, 2048, 1536, 2, 16)),
+                                   ("cfg5", (4, 2048, 2048, 2, 64))):
+        g = torch.Generator(device="cuda").manual_seed(11)
+        shapes = ((B, T, C), (B, T, C, K), (B, T, C, K + 1), (B, T, C), (B, T, M),
+                  (B, T, K + 1, M), (B, T, C, K))
+        tensors = [(torch.randn(*shape, device="cuda", generator=g) * 0.15).to(bf).requires_grad_()
+                   for shape in shapes]
+        dy = torch.randn(B, T, C, device="cuda", generator=g).to(bf)
+        stream = torch.cuda.current_stream()
+
+        def forward():
+            x, alpha, rho, gamma, write, read, beta = tensors
+            return mira.matrix_lattice_iir(x, alpha, rho, gamma, write, read, raw_beta=beta)
+
+        def step():
+            forward().backward(dy)
+
+        for _ in range(warmup):
+            step()
+        times = {}
+        for name, fn in (("forward", forward), ("step", step)):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            end.record(stream)
+            torch.cuda.synchronize()
+            times[name] = start.elapsed_time(end) * 1e-3 / steps
+        for t in tensors:
+            t.grad = None
+        backward_s = times["step"] - times["forward"]
+        results[label] = {
+            "shape": f"B={B} T={T} C={C} K={K} M={M}", "tokens": B * T,
+            "forward_us": round(times["forward"] * 1e6, 1),
+            "backward_us": round(backward_s * 1e6, 1),
+            "step_us": round(times["step"] * 1e6, 1),
+            "tokens_per_s": round(B * T / times["step"], 1),
+            "backward_over_forward": round(backward_s / times["forward"], 3)}
+    return results
+
+
 def stack_leg(torch, steps, warmup):
     """24 random-init MiraBlocks (d_model 2048, lattice_d_e 2048, K=2,
     d_m 64, d_r 128, FFN 8192 SiLU-MLP), vocab 32000 with the tied head, weights N(0, 0.02^2),
@@ -440,39 +574,91 @@ def decode_through_cache(torch, model, vocab, prompt=64, new=24):
     return results
 
 
-def cpu_leg(budget_s=12.0):
-    """The oracle's restatement of the reference CPU mixer (the batched per-token formulation of
-    model/mira_mixer.py:319-387, numpy float32) on the cfg2 workload realised as the K=1 lattice,
-    plus the conv: one sequence x 2048 channels, streamed in blocks of 2048 tokens that carry the
-    scan state and the conv ring, until about `budget_s` seconds of CPU time are spent."""
+def _cpu_sample(channels, tokens, seed, block=2048):
+    """The oracle's restatement of the reference CPU mixer (the batched per-token formulation
+    of model/mira_mixer.py:319-387, numpy float32) on `channels` channels of one cfg2 sequence
+    of `tokens` tokens, realised as the K=1 lattice with the conv in front, in blocks that carry
+    the scan state and the conv ring. Inputs are drawn first; returns the compute seconds."""
     import numpy as np
 
     from oracle import baseline as Bl
     from oracle import lattice as L
 
+    rng = np.random.default_rng(seed)
+    _, _, w, bias, h0 = Bl.diag_inputs(rng, 1, 1, channels, h0_scale=0.1)
+    blocks = [Bl.diag_inputs(rng, 1, min(block, tokens - first), channels)[:2]
+              for first in range(0, tokens, block)]
+    state = h0.reshape(1, 1, channels, 1).astype(np.float32)
+    ring = np.zeros((1, channels, 3), np.float32)
+    seconds, position = 0.0, 0
+    for x, a in blocks:
+        t0 = time.perf_counter()
+        u = Bl.causal_conv(x, w, bias, ring=ring, pos=position, dtype=np.float32).astype(np.float32)
+        inputs = Bl.diag_as_lattice(u, a)
+        _, state = L.lattice_scan_batched(*inputs[:7], state=state)
+        seconds += time.perf_counter() - t0
+        ring = Bl.ring_after(x.astype(np.float32), ring, position)
+        position += x.shape[1]
+    return seconds
+
+
+def _cpu_worker(job):
     from threadpoolctl import threadpool_limits
 
-    rng = np.random.default_rng(0)
-    block, D = 2048, 2048
-    _, _, w, bias, h0 = Bl.diag_inputs(rng, 1, 1, D, h0_scale=0.1)
-    state = h0.reshape(1, 1, D, 1).astype(np.float32)
-    ring = np.zeros((1, D, 3), np.float32)
-    tokens, seconds = 0, 0.0
-    while seconds < budget_s and tokens < 64 * block:
-        x, a, _, _, _ = Bl.diag_inputs(rng, 1, block, D)
-        with threadpool_limits(limits=1):                           # one core, BLAS included
-            t0 = time.perf_counter()
-            u = Bl.causal_conv(x, w, bias, ring=ring, pos=tokens, dtype=np.float32).astype(np.float32)
-            inputs = Bl.diag_as_lattice(u, a)
-            _, state = L.lattice_scan_batched(*inputs[:7], state=state)
-            seconds += time.perf_counter() - t0
-        ring = Bl.ring_after(x.astype(np.float32), ring, tokens)
-        tokens += block
-    return {"value": tokens / seconds, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"1 sequence x {tokens} tokens x {D} channels (cfg2 geometry, fp32, oracle "
-                      f"batched lattice restatement + conv, blocks of {block} tokens carrying the "
-                      f"state and ring), {seconds:.1f} s of numpy single-threaded time on a host with "
-                      f"{os.cpu_count()} cores"}
+    with threadpool_limits(limits=1):
+        return _cpu_sample(*job)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as handle:
+            for line in handle:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_leg(tokens=8192, channels=2048, runs=3):
+    """The CPU baseline: the oracle restatement of the reference CPU
+    mixer on one cfg2 sequence of `tokens` tokens x `channels` channels, one warm-up and then
+    the median of `runs` runs, once on one thread and once on all the host cores this job may
+    use (the scan is independent per channel, so each worker process takes an equal channel
+    slice; a run lasts as long as its slowest worker). Worker processes are started fresh (spawn)
+    and touch no GPU."""
+    import multiprocessing
+    import statistics
+
+    import numpy as np
+    import torch
+
+    from threadpoolctl import threadpool_limits
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    with threadpool_limits(limits=1):
+        _cpu_sample(channels, 512, 99)                                   # warm-up
+        single = statistics.median(_cpu_sample(channels, tokens, seed) for seed in range(runs))
+    width = channels // cores
+    with multiprocessing.get_context("spawn").Pool(cores) as pool:
+        pool.map(_cpu_worker, [(width, 512, 99)] * cores)                # warm-up
+        walls = []
+        for seed in range(runs):
+            walls.append(max(pool.map(_cpu_worker, [(width, tokens, seed * 100 + i)
+                                                    for i in range(cores)])))
+    parallel = statistics.median(walls)
+    covered = width * cores
+    return {"value": tokens * covered / channels / parallel, "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"1 sequence x {tokens} tokens x {channels} channels of the cfg2 workload "
+                      f"(fp32; the oracle's batched restatement of the reference CPU mixer on the "
+                      f"K=1 lattice realisation, conv in front, blocks of 2048 tokens carrying "
+                      f"state and ring): {cores} worker processes of {width} channels each, one "
+                      f"warm-up, median of {runs} runs ({parallel:.2f} s)",
+            "single_thread": {"value": tokens / single, "unit": "tokens/s", "cores": 1,
+                              "seconds": round(single, 2)},
+            "method": f"one warm-up, median of {runs}", "cpu_model": _cpu_model(),
+            "host_cpus": os.cpu_count(), "numpy": np.__version__, "torch": torch.__version__}
 
 
 def main():
@@ -482,6 +668,12 @@ def main():
                                    "batch and channels with no exchange, and no multi-GPU leg "
                                    "is built or measured", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.traffic_child:
+        traffic_child()
+        return
+    # the headline kernel's HBM traffic, from child rocprofv3 runs started before this process
+    # initialises the GPU
+    traffic, traffic_note = (None, "skipped (--no-traffic)") if args.no_traffic else measure_traffic()
     import torch
 
     from mira_amd import _lib, mira
@@ -489,16 +681,17 @@ def main():
     if not torch.cuda.is_available() or _lib.library() is None:
         print(json.dumps({"error": f"needs a HIP device and the built library: {_lib.why()}"}))
         sys.exit(1)
+    legs = (set(args.only) & set(LEGS)) if args.only else set(LEGS)
+    if args.no_stack:
+        legs.discard("stack")
     prefill = prefill_leg(torch, mira, args.steps, args.warmup)
-    decode = decode_leg(torch, mira, args.decode_steps)
-    gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3)
-    gla_hbm = gla["algorithmic"] / gla["kernel_s"] / 1e9
-    lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2)
-    ctl = control_leg(torch, mira, max(5, args.steps // 10), 3)
-    stack = None if args.no_stack else stack_leg(torch, 3, 1)
+    decode = decode_leg(torch, mira, args.decode_steps) if "decode" in legs else None
+    gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3) if "gla" in legs else None
+    lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2) if "lattice" in legs else None
+    ctl = control_leg(torch, mira, max(5, args.steps // 10), 3) if "control" in legs else None
+    back = backward_leg(torch, mira, max(3, args.steps // 10), 2) if "backward" in legs else None
+    stack = stack_leg(torch, 3, 1) if "stack" in legs else None
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
-    traffic = traffic_from_profiles("diag_column_kernel")
-    gla_achieved = decode["gla_bytes"] / decode["gla_kernel_s"] / 1e9
     line = {
         "metric": METRIC,
         "value": prefill["tokens"] * args.steps / prefill["elapsed"],
@@ -512,10 +705,20 @@ def main():
                    "global_batch": 8, "seq_len": 4096, "channels": 2048, "parallelism": "none"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "diag_column_kernel",
+                     "traffic": None if traffic is None else traffic["bytes"],
+                     "kernel": "diag_column_kernel",
                      "kernel_us": round(prefill["kernel_s"] * 1e6, 2),
-                     "algorithmic_bytes": prefill["algorithmic"]},
-        "decode": {"metric": "decode steps/s at batch 256", "unit": "steps/s",
+                     "algorithmic_bytes": prefill["algorithmic"],
+                     "traffic_source": ("measured in this run: rocprofv3 --pmc FETCH_SIZE, then "
+                                        "WRITE_SIZE, over `bench.py --traffic-child`, each scaled "
+                                        "by its reading for a 128 MiB + 128 MiB copy")
+                     if traffic is not None else f"not measured: {traffic_note}",
+                     "traffic_detail": traffic},
+        "watchdog": prefill["watchdog"],
+    }
+    if decode is not None:
+        gla_achieved = decode["gla_bytes"] / decode["gla_kernel_s"] / 1e9
+        line["decode"] = {"metric": "decode steps/s at batch 256", "unit": "steps/s",
                    "value": decode["steps"] / decode["graph_elapsed"], "steps": decode["steps"],
                    "launch": "the steps' launches replayed as one HIP graph, each step's "
                              "conv+diag launch on a side stream beside its GLA launch",
@@ -531,23 +734,24 @@ def main():
                    "roofline": {"bound": "hbm", "kernel": "gla_step_kernel",
                                 "achieved": round(gla_achieved, 1), "peak": HBM_PEAK_GBS,
                                 "unit": "GB/s", "frac": round(gla_achieved / HBM_PEAK_GBS, 4),
-                                "traffic": traffic_from_profiles("gla_step_kernel"),
                                 "kernel_us": round(decode["gla_kernel_s"] * 1e6, 2),
-                                "algorithmic_bytes": decode["gla_bytes"]}},
-        "matrix_state_prefill": {
+                                "algorithmic_bytes": decode["gla_bytes"]}}
+    if gla is not None:
+        gla_hbm = gla["algorithmic"] / gla["kernel_s"] / 1e9
+        line["matrix_state_prefill"] = {
             "metric": "GLA chunked prefill tokens/s (cfg3: B=4 T=8192 H=16 d=128 bf16, chunk 64)",
             "unit": "tokens/s", "value": gla["tokens"] * gla["steps"] / gla["elapsed"],
             "roofline": {"bound": "hbm", "kernel": "gla_chunk_kernel",
                          "achieved": round(gla_hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gla_hbm / HBM_PEAK_GBS, 4),
-                         "traffic": traffic_from_profiles("gla_chunk_kernel"),
                          "kernel_us": round(gla["kernel_s"] * 1e6, 2),
                          "algorithmic_bytes": gla["algorithmic"]},
             "mfma": {"achieved": round(gla["flops"] / gla["kernel_s"] / 1e12, 1),
                      "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(gla["flops"] / gla["kernel_s"] / 1e12 / 2500.0, 4),
-                     "flops": gla["flops"]}},
-        "lattice_operator": {
+                     "flops": gla["flops"]}}
+    if lat is not None:
+        line["lattice_operator"] = {
             "metric": "matrix_lattice_iir tokens/s at the cfg5 mixer geometry, bf16",
             "shape": lat["shape"], "unit": "tokens/s", "value": lat["tokens"] / lat["call_s"],
             "call_us": round(lat["call_s"] * 1e6, 1),
@@ -566,8 +770,9 @@ def main():
                              "achieved": round(lat["step_bytes"] / lat["step_s"] / 1e9, 1),
                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(lat["step_bytes"] / lat["step_s"] / 1e9 / HBM_PEAK_GBS, 4),
-                             "algorithmic_bytes": lat["step_bytes"]}}},
-        "control_scan": {
+                             "algorithmic_bytes": lat["step_bytes"]}}}
+    if ctl is not None:
+        line["control_scan"] = {
             "metric": "matrix_lattice_iir_control tokens/s at the reference mixer geometry, bf16, "
                       "coefficients formed inside the scan",
             "shape": ctl["shape"], "unit": "tokens/s", "value": ctl["tokens"] / ctl["call_s"],
@@ -584,9 +789,11 @@ def main():
             "valu": {"achieved": round(ctl["flops"] / ctl["kernel_s"] / 1e12, 1),
                      "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(ctl["flops"] / ctl["kernel_s"] / 1e12 / 157.3, 4),
-                     "flops": ctl["flops"]}},
-        "watchdog": prefill["watchdog"],
-    }
+                     "flops": ctl["flops"]}}
+    if back is not None:
+        line["training_scan"] = dict(
+            back, metric="matrix_lattice_iir forward + backward (all seven gradients) tokens/s, "
+                         "bf16, zero initial state")
     if stack is not None:
         line["stack"] = {
             "metric": "cfg5 forward prefill tokens/s (24 MiraBlocks, bf16, no cache)",
@@ -602,11 +809,7 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_leg()
     if args.calibrate:
-        source = torch.ones(64 << 20, device="cuda", dtype=torch.bfloat16)
-        target = torch.empty_like(source)
-        for _ in range(5):
-            torch.add(source, 1.0, out=target)
-        torch.cuda.synchronize()
+        calibrate(torch, 5)
     print(json.dumps(line), flush=True)
 
 
