@@ -14,7 +14,8 @@ sample of the same workload. Also reported, not headline: the GLA chunked prefil
 (K=2, M=64), matrix_lattice_iir_control (coefficients formed inside the scan) at the
 reference's own mixer geometry against its materialised path, and the 24-layer MiraLLM forward
 of `configs[4]` with the mixer's and the scan's share of its time (skip it with --no-stack), and a
-training step of the scan (forward + backward) at the reference's mira-s and the cfg5 geometry.
+training step of the scan (forward + backward) at the reference's mira-s and the cfg5 geometry,
+and the MiraMixer module at the shapes the reference quotes its own mixer numbers for.
 The headline kernel's HBM traffic is measured in the same run by two rocprofv3 --pmc child runs
 (FETCH_SIZE, WRITE_SIZE) started before this process initialises the GPU (skip with
 --no-traffic). `--only LEG` runs the headline plus the named legs (`--only prefill`: the headline
@@ -33,7 +34,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "official-mira-llm_amd"))
 
 HBM_PEAK_GBS = 8000.0
-LEGS = ("decode", "gla", "lattice", "control", "backward", "stack")
+LEGS = ("decode", "gla", "lattice", "control", "backward", "mixer", "stack")
 ONLY = ("prefill",) + LEGS
 CALIBRATION_KERNEL = "neg_kernel"                 # torch.neg over 64 Mi bf16 elements:
 CALIBRATION_KIB = 131072.0                         # it reads 128 MiB and writes 128 MiB
@@ -463,6 +464,45 @@ def backward_leg(torch, mira, steps, warmup):
     return results
 
 
+def mixer_leg(torch, mira, steps, warmup):
+    """The MiraMixer module (projections, control SiLU, the scan, gate, out_proj) at the reference's
+    mira-s mixer geometry (width 768, d_e 1536, K 2, d_m 16, d_r 48, bf16, eval, no cache) and the
+    shapes its own numbers are quoted at: one 32,768-token sequence (forward latency), and the
+    profiler's maximum-batch calls of ~1.18 M tokens at T = 2,048 (B = 574) and T = 32,768
+    (B = 36) (kernel/cuda/mira_dspv2/README.md:41-49). The reference's figures are RTX A6000 /
+    RTX 6000 Ada measurements and simulations: context, not a target."""
+    from mira_amd.mixer import MiraMixer
+
+    d, C, K, M, R = 768, 1536, 2, 16, 48
+    torch.manual_seed(9)
+    mixer = MiraMixer(d, K, C, R, M).to("cuda", torch.bfloat16).eval()
+    stream = torch.cuda.current_stream()
+    results = {}
+    for B, T in ((1, 32768), (574, 2048), (36, 32768)):
+        x = torch.randn(B, T, d, device="cuda", dtype=torch.bfloat16)
+        with torch.no_grad():
+            for _ in range(warmup):
+                mixer(x)
+            before = dict(mira.usage())
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(steps):
+                mixer(x)
+            end.record(stream)
+            torch.cuda.synchronize()
+        seconds = start.elapsed_time(end) * 1e-3 / steps
+        fused = mira.usage()["control"] > before["control"]
+        results[f"B{B}_T{T}"] = {"tokens": B * T, "ms": round(seconds * 1e3, 3),
+                                 "tokens_per_s": round(B * T / seconds, 1),
+                                 "scan": "coefficients formed in the scan" if fused
+                                 else "coefficient GEMM + chunked scan"}
+        del x
+    del mixer
+    torch.cuda.empty_cache()
+    return results
+
+
 def stack_leg(torch, steps, warmup):
     """24 random-init MiraBlocks (d_model 2048, lattice_d_e 2048, K=2,
     d_m 64, d_r 128, FFN 8192 SiLU-MLP), vocab 32000 with the tied head, weights N(0, 0.02^2),
@@ -690,6 +730,7 @@ def main():
     lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2) if "lattice" in legs else None
     ctl = control_leg(torch, mira, max(5, args.steps // 10), 3) if "control" in legs else None
     back = backward_leg(torch, mira, max(3, args.steps // 10), 2) if "backward" in legs else None
+    mix = mixer_leg(torch, mira, 3, 1) if "mixer" in legs else None
     stack = stack_leg(torch, 3, 1) if "stack" in legs else None
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
     line = {
@@ -794,6 +835,14 @@ def main():
         line["training_scan"] = dict(
             back, metric="matrix_lattice_iir forward + backward (all seven gradients) tokens/s, "
                          "bf16, zero initial state")
+    if mix is not None:
+        line["mixer_module"] = dict(
+            mix, metric="MiraMixer forward tokens/s at the reference's mira-s geometry (d 768, "
+                        "d_e 1536, K 2, d_m 16, d_r 48), bf16, eval",
+            reference_context="published for the mixer module on an RTX A6000 at 32,768 tokens: "
+                              "11.37 ms forward, 8.36 M tokens/s at maximum batch "
+                              "(doc/html/pages/results.html); simulated RTX 6000 Ada max-batch "
+                              "8.70-11.03 M tokens/s (kernel/cuda/mira_dspv2/README.md:41-49)")
     if stack is not None:
         line["stack"] = {
             "metric": "cfg5 forward prefill tokens/s (24 MiraBlocks, bf16, no cache)",
