@@ -25,7 +25,8 @@
 //                     caller wants the gradient of the raw write).
 // The chunk is short (<= 16 tokens) so that a lane keeps the state entering every token of its
 // chunk in registers (<= 128 floats). Per-(token, channel) sums over a channel's lanes use DPP;
-// per-(token, slot) sums over the channels of a block go through LDS.
+// per-(token, slot) sums over the channels of a block are first added across a 16-lane row's
+// channels with DPP, then go through a double-buffered LDS tile (one barrier a token).
 #include "lattice_common.hpp"
 #include "mira_abi_internal.hpp"
 
@@ -223,35 +224,40 @@ __global__ __launch_bounds__(BLOCK) void lattice_adjoint_combine(LatticeBackArgs
     const int m = index % a.M;
     const int c = (index / a.M) % a.C;
     const int b = index / ((long long)a.M * a.C);
-    float run[K];
+    // chunk j's adjoint summary and transition do not depend on the running adjoint, so they
+    // are loaded one chunk ahead of the serial chain
+    const long long stride = (long long)a.C;                      // planes per chunk
+    const long long plane0 = (long long)b * a.chunks * a.C + c;   // chunk 0's plane
+    float run[K], summary[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) run[k] = 0.0f;
-    for (int j = a.chunks - 1; j >= 0; --j) {
-        const long long plane = ((long long)b * a.chunks + j) * a.C + c;
-        float summary[K];
+    const int last = a.chunks - 1;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            float *slot_k = a.adjoint + (plane * K + k) * a.M + m;
-            summary[k] = j > 0 ? *slot_k : 0.0f;
-            *slot_k = run[k];                                  // the adjoint at chunk j's end
-        }
+    for (int k = 0; k < K; ++k)
+        summary[k] = last > 0 ? a.adjoint[((plane0 + last * stride) * K + k) * a.M + m] : 0.0f;
+    for (int j = last; j >= 0; --j) {
+        const long long plane = plane0 + j * stride;
+        // the next (earlier) chunk's summary and this chunk's transition, ahead of their use
+        float ahead[K], transition[K * K];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            ahead[k] = j > 1 ? a.adjoint[((plane - stride) * K + k) * a.M + m] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < K * K; ++q)
+            transition[q] = (j > 0 && j < last) ? a.phi[plane * K * K + q] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) a.adjoint[(plane * K + k) * a.M + m] = run[k];   // chunk j's end
         if (j == 0) break;
         float next[K];
-        if (j == a.chunks - 1) {
 #pragma unroll
-            for (int k = 0; k < K; ++k) next[k] = summary[k];   // run is zero: Phi^T run = 0
-        } else {
-            const float *phi = a.phi + plane * K * K;
+        for (int jj = 0; jj < K; ++jj) {
+            float value = summary[jj];
 #pragma unroll
-            for (int jj = 0; jj < K; ++jj) {
-                float value = summary[jj];
-#pragma unroll
-                for (int i = 0; i < K; ++i) value = fmaf(phi[i * K + jj], run[i], value);
-                next[jj] = value;
-            }
+            for (int i = 0; i < K; ++i) value = fmaf(transition[i * K + jj], run[i], value);
+            next[jj] = value;                  // at the last chunk run is zero and so is Phi^T run
         }
 #pragma unroll
-        for (int k = 0; k < K; ++k) run[k] = next[k];
+        for (int k = 0; k < K; ++k) { run[k] = next[k]; summary[k] = ahead[k]; }
     }
 }
 
@@ -266,11 +272,14 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
                                             // then the sums d rc[K], d rs[K], P[K+1], dx
     constexpr int NS = (K + 2) * M;         // s, nu_0 .. nu_K of a token
     constexpr int NO = (K + 2) * M;         // per-token channel sums: ds, dnu_0 .. dnu_K
-    constexpr int TPO = (BLOCK / NO >= G) ? G : (BLOCK / NO >= 1 ? BLOCK / NO : 1);
+    // rows of partial channel sums a token leaves in LDS: a 16-lane row first adds its channels
+    // with DPP (narrow channels), so one row of 16 lanes, or one wide channel, writes each set
+    constexpr int RG = L < 16 ? BLOCK / 16 : G;
+    constexpr int TPO = (BLOCK / NO >= RG) ? RG : (BLOCK / NO >= 1 ? BLOCK / NO : 1);
     constexpr int TPO2 = (TPO >= 32) ? 32 : (TPO >= 16) ? 16 : (TPO >= 8) ? 8 : (TPO >= 4) ? 4
                                                             : (TPO >= 2) ? 2 : 1;
     constexpr int PER_PASS = BLOCK / TPO2;
-    static_assert((S * NS + S * NQ * G + G * NO) * 4 + S <= 65536, "LDS budget");
+    static_assert((S * NS + S * NQ * G + 2 * RG * NO) * 4 + S <= 65536, "LDS budget");
     int block = blockIdx.x;
     const int group = block % a.groups;
     block /= a.groups;
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
 
     __shared__ float s_sn[S * NS];
     __shared__ float s_tc[S * NQ * G];
-    __shared__ float s_red[G * NO];
+    __shared__ __align__(16) float s_red[2][RG * NO];   // double-buffered: one barrier a token
     __shared__ unsigned char s_valid[S];
     const IO *write = static_cast<const IO *>(a.write);
     const IO *read = static_cast<const IO *>(a.read);
@@ -409,12 +418,32 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
 #pragma unroll
             for (int q = 0; q < NQ; ++q) s_tc[(t * NQ + q) * G + cl] = sums[q];
         }
-        // per (token, slot): the channel group's sums through LDS
+        // per (token, slot): the channel group's sums -- a row's channels added with DPP, then
+        // one set per row (or per wide channel) through LDS, double-buffered by token parity
+        float *red_buffer = s_red[t & 1];
+        const int rowgroup = L < 16 ? (int)threadIdx.x / 16 : cl;
+        const bool writer = L < 16 ? ((int)threadIdx.x % 16) < L : true;
 #pragma unroll
-        for (int kk = 0; kk < K + 2; ++kk)
+        for (int kk = 0; kk < K + 2; ++kk) {
 #pragma unroll
-            for (int v = 0; v < MV; ++v)
-                s_red[cl * NO + kk * M + slot<M, L>(lane, v)] = active ? red[kk][v] : 0.0f;
+            for (int v = 0; v < MV; ++v) {
+                float value = active ? red[kk][v] : 0.0f;
+                if constexpr (L < 16) value = row_channel_sum<L>(value);
+                red[kk][v] = value;
+            }
+            if (writer) {
+                float *dst = red_buffer + rowgroup * NO + kk * M;
+                if constexpr (MV % 4 == 0) {
+#pragma unroll
+                    for (int v = 0; v < MV; v += 4)
+                        *reinterpret_cast<float4 *>(dst + slot<M, L>(lane, v)) =
+                            make_float4(red[kk][v], red[kk][v + 1], red[kk][v + 2], red[kk][v + 3]);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < MV; ++v) dst[slot<M, L>(lane, v)] = red[kk][v];
+                }
+            }
+        }
         __syncthreads();
         const long long out_row = ((long long)group * a.B + b) * a.T + first + t;
 #pragma unroll
@@ -422,11 +451,10 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
             const int o = o0 + threadIdx.x / TPO2, part = threadIdx.x % TPO2;
             float total = 0.0f;
             if (o < NO)
-                for (int g = part; g < G; g += TPO2) total += s_red[g * NO + o];
+                for (int g = part; g < RG; g += TPO2) total += red_buffer[g * NO + o];
             total = group_sum<TPO2>(total);
             if (o < NO && part == 0) a.partial[out_row * NO + o] = total;
         }
-        __syncthreads();
     }
 
     // per (token, channel) gradients, one thread per pair

@@ -29,18 +29,36 @@ __device__ __forceinline__ int slot(int lane, int v) {
     else return v * L + lane;
 }
 
-// Sum over the L lanes of a channel group (adjacent lanes): cross-lane DPP within a quad,
-// then butterflies through the LDS crossbar for wider groups.
+// DPP lane movement within a 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                              0xf, 0xf, false));
+}
+
+// Sum over the L lanes of a channel group (adjacent, aligned lanes), in every lane of the group:
+// quad permutes for the first two steps, then the row's half-mirror (lane i <-> 7 - i) and mirror
+// (i <-> 15 - i), which pair each quad or half-row with the other one of its group, all as DPP
+// operands of the add; only groups wider than a row go through the LDS crossbar.
 template <int L>
 __device__ __forceinline__ float lane_sum(float v) {
-    if constexpr (L >= 2)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
-                                                                0xB1, 0xf, 0xf, false));
-    if constexpr (L >= 4)
-        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
-                                                                0x4E, 0xf, 0xf, false));
+    if constexpr (L >= 2) v += dpp<0xB1>(v);            // quad_perm [1,0,3,2]
+    if constexpr (L >= 4) v += dpp<0x4E>(v);            // quad_perm [2,3,0,1]
+    if constexpr (L >= 8) v += dpp<0x141>(v);           // row_half_mirror
+    if constexpr (L >= 16) v += dpp<0x140>(v);          // row_mirror
 #pragma unroll
-    for (int offset = 4; offset < L; offset <<= 1) v += __shfl_xor(v, offset, 64);
+    for (int offset = 16; offset < L; offset <<= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+// Sum over the channels of a 16-lane row whose channels are L lanes apart (L < 16), in every
+// lane: row rotations by 8, 4, ... L, each the DPP operand of the add.
+template <int L>
+__device__ __forceinline__ float row_channel_sum(float v) {
+    if constexpr (L < 16) v += dpp<0x128>(v);           // row_ror:8
+    if constexpr (L < 8) v += dpp<0x124>(v);            // row_ror:4
+    if constexpr (L < 4) v += dpp<0x122>(v);            // row_ror:2
+    if constexpr (L < 2) v += dpp<0x121>(v);            // row_ror:1
     return v;
 }
 
