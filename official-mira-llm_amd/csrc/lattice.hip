@@ -455,27 +455,42 @@ __global__ __launch_bounds__(BLOCK) void lattice_combine(LatticeArgs a) {
 #pragma unroll
     for (int k = 0; k < K; ++k)
         S[k] = a.state_in ? a.state_in[(((long long)b * K + k) * a.C + c) * a.M + m] : 0.0f;
-    for (int j = 0; j < a.chunks; ++j) {
-        const long long plane = ((long long)b * a.chunks + j) * a.C + c;
-        float carry[K];
+    // The chunk maps do not depend on the running state: they are loaded D chunks at a time
+    // ahead of the serial chain, so a long chain (training runs 16-token chunks) waits on memory
+    // once per D chunks instead of once per chunk.
+    constexpr int D = 8;
+    for (int j0 = 0; j0 < a.chunks; j0 += D) {
+        float carry[D][K], phi[D][K * K];
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            float *slot_k = a.carry + (plane * K + k) * a.M + m;
-            carry[k] = (j + 1 < a.chunks) ? *slot_k : 0.0f;
-            *slot_k = S[k];
-        }
-        if (j + 1 == a.chunks) break;
-        const float *phi = a.phi + plane * K * K;
-        float next[K];
+        for (int d = 0; d < D; ++d) {
+            const int j = j0 + d;
+            const bool summarised = j + 1 < a.chunks;
+            const long long plane = ((long long)b * a.chunks + j) * a.C + c;
 #pragma unroll
-        for (int i = 0; i < K; ++i) {
-            float value = carry[i];
+            for (int k = 0; k < K; ++k)
+                carry[d][k] = summarised ? a.carry[(plane * K + k) * a.M + m] : 0.0f;
 #pragma unroll
-            for (int jj = 0; jj < K; ++jj) value = fmaf(phi[i * K + jj], S[jj], value);
-            next[i] = value;
+            for (int q = 0; q < K * K; ++q) phi[d][q] = summarised ? a.phi[plane * K * K + q] : 0.0f;
         }
 #pragma unroll
-        for (int k = 0; k < K; ++k) S[k] = next[k];
+        for (int d = 0; d < D; ++d) {
+            const int j = j0 + d;
+            if (j < a.chunks) {
+                const long long plane = ((long long)b * a.chunks + j) * a.C + c;
+#pragma unroll
+                for (int k = 0; k < K; ++k) a.carry[(plane * K + k) * a.M + m] = S[k];
+                float next[K];
+#pragma unroll
+                for (int i = 0; i < K; ++i) {
+                    float value = carry[d][i];
+#pragma unroll
+                    for (int jj = 0; jj < K; ++jj) value = fmaf(phi[d][i * K + jj], S[jj], value);
+                    next[i] = value;
+                }
+#pragma unroll
+                for (int k = 0; k < K; ++k) S[k] = next[k];
+            }
+        }
     }
 }
 

@@ -225,39 +225,48 @@ __global__ __launch_bounds__(BLOCK) void lattice_adjoint_combine(LatticeBackArgs
     const int c = (index / a.M) % a.C;
     const int b = index / ((long long)a.M * a.C);
     // chunk j's adjoint summary and transition do not depend on the running adjoint, so they
-    // are loaded one chunk ahead of the serial chain
-    const long long stride = (long long)a.C;                      // planes per chunk
+    // are loaded D chunks at a time ahead of the serial chain (a wait on memory once per D
+    // chunks, not once per chunk)
+    constexpr int D = 8;
     const long long plane0 = (long long)b * a.chunks * a.C + c;   // chunk 0's plane
-    float run[K], summary[K];
+    const long long stride = (long long)a.C;                      // planes per chunk
+    const int last = a.chunks - 1;
+    float run[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) run[k] = 0.0f;
-    const int last = a.chunks - 1;
+    for (int j0 = last; j0 >= 0; j0 -= D) {
+        float summary[D][K], transition[D][K * K];
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-        summary[k] = last > 0 ? a.adjoint[((plane0 + last * stride) * K + k) * a.M + m] : 0.0f;
-    for (int j = last; j >= 0; --j) {
-        const long long plane = plane0 + j * stride;
-        // the next (earlier) chunk's summary and this chunk's transition, ahead of their use
-        float ahead[K], transition[K * K];
+        for (int d = 0; d < D; ++d) {
+            const int j = j0 - d;
+            const long long plane = plane0 + j * stride;
 #pragma unroll
-        for (int k = 0; k < K; ++k)
-            ahead[k] = j > 1 ? a.adjoint[((plane - stride) * K + k) * a.M + m] : 0.0f;
+            for (int k = 0; k < K; ++k)
+                summary[d][k] = j > 0 ? a.adjoint[(plane * K + k) * a.M + m] : 0.0f;
 #pragma unroll
-        for (int q = 0; q < K * K; ++q)
-            transition[q] = (j > 0 && j < last) ? a.phi[plane * K * K + q] : 0.0f;
-#pragma unroll
-        for (int k = 0; k < K; ++k) a.adjoint[(plane * K + k) * a.M + m] = run[k];   // chunk j's end
-        if (j == 0) break;
-        float next[K];
-#pragma unroll
-        for (int jj = 0; jj < K; ++jj) {
-            float value = summary[jj];
-#pragma unroll
-            for (int i = 0; i < K; ++i) value = fmaf(transition[i * K + jj], run[i], value);
-            next[jj] = value;                  // at the last chunk run is zero and so is Phi^T run
+            for (int q = 0; q < K * K; ++q)
+                transition[d][q] = (j > 0 && j < last) ? a.phi[plane * K * K + q] : 0.0f;
         }
 #pragma unroll
-        for (int k = 0; k < K; ++k) { run[k] = next[k]; summary[k] = ahead[k]; }
+        for (int d = 0; d < D; ++d) {
+            const int j = j0 - d;
+            if (j >= 0) {
+                const long long plane = plane0 + j * stride;
+#pragma unroll
+                for (int k = 0; k < K; ++k) a.adjoint[(plane * K + k) * a.M + m] = run[k];   // j's end
+                // at the last chunk run is zero, and so is Phi^T run
+                float next[K];
+#pragma unroll
+                for (int jj = 0; jj < K; ++jj) {
+                    float value = summary[d][jj];
+#pragma unroll
+                    for (int i = 0; i < K; ++i) value = fmaf(transition[d][i * K + jj], run[i], value);
+                    next[jj] = value;
+                }
+#pragma unroll
+                for (int k = 0; k < K; ++k) run[k] = next[k];
+            }
+        }
     }
 }
 
