@@ -54,7 +54,7 @@ class _CapturedStep:
         with torch.cuda.stream(side):
             model(self.ids, cache=cache)                 # warm-up outside the capture
         torch.cuda.current_stream(device).wait_stream(side)
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=side):      # the warm-up's stream
             self.logits = model(self.ids, cache=cache).logits[:, -1]
         for held, keep in zip(cache.state, saved):
             if held is not None:

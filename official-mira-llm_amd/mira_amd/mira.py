@@ -460,6 +460,16 @@ def _control_plan(x, control, weight, bias, gamma, memory_write, order, memory):
     return row, gamma_row
 
 
+def control_scan_serves(batch, tokens, channels, order, memory, rank, dtype, device_index=None):
+    """Whether the coefficient-forming scan has a kernel for this geometry (bf16 only); a
+    caller that holds the coefficient weights can then take the GEMM + scan route itself when
+    it does not (mira_lattice_control_serves)."""
+    if dtype != torch.bfloat16 or not status(device_index)[0]:
+        return False
+    return bool(_lib.require().mira_lattice_control_serves(batch, tokens, channels, order, memory,
+                                                           rank, _lib.BF16))
+
+
 def matrix_lattice_iir_control(x, control, coefficient_weight, coefficient_bias, spans, gamma,
                                memory_write, valid=None, state=None, return_state=False,
                                arch="cauchy_x_hyperbolic"):

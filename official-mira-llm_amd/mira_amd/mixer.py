@@ -26,6 +26,8 @@ from . import mira as plugin
 from . import prefix_cache
 
 ARCHES = tuple(plugin.ARCH_STAGE)
+# tokens from which the inference input projection runs as two GEMMs instead of one
+SPLIT_ROWS = 1024
 
 
 def _declined(signal, order, memory_dimension):
@@ -57,10 +59,24 @@ def _packing_signature(normalized_x, projections):
     parameters = [t for p in projections for t in (p.weight, p.bias) if t is not None]
     if not all(type(t) is nn.Parameter for t in parameters):
         return None
-    stream = (torch.cuda.current_stream(normalized_x.device).cuda_stream
-              if normalized_x.is_cuda else None)
-    return (tuple((id(t), t.data_ptr(), t._version, t.dtype, t.device, tuple(t.shape),
-                   tuple(t.stride())) for t in parameters), stream)
+    return tuple((id(t), t.data_ptr(), t._version, t.dtype, t.device, tuple(t.shape),
+                  tuple(t.stride())) for t in parameters)
+
+
+def _used_on_this_stream(kept, reference):
+    """Tell the caching allocator that the kept weight tensors are read on the current stream
+    (once per stream; not while a graph is being captured, whose launches own no memory), so
+    that memory they free on a rebuild is not handed out again while that stream may still
+    read it. The weights are kept across streams instead of being rebuilt per stream: a
+    rebuild inside a graph capture would replay its copies at every step."""
+    if not reference.is_cuda or torch.cuda.is_current_stream_capturing():
+        return
+    stream = torch.cuda.current_stream(reference.device)
+    if stream.cuda_stream in kept["streams"]:
+        return
+    for tensor in kept["tensors"]:
+        tensor.record_stream(stream)
+    kept["streams"].add(stream.cuda_stream)
 
 
 class MiraMixer(nn.Module):
@@ -122,36 +138,117 @@ class MiraMixer(nn.Module):
         would do exactly the same: a plain torch.Tensor input, no global module hooks, and three
         plain nn.Linear projections with no hooks, no replaced forward and plain nn.Parameter
         weights. The packed weight is rebuilt whenever any parameter's identity, storage,
-        version, dtype, device, shape or strides change, or the call runs on another stream.
-        Otherwise (and with gradients) the three modules are called."""
-        projections = (self.input_projection, self.to_gate, self.to_control)
+        version, dtype, device, shape or strides change; it serves every stream. Otherwise (and
+        with gradients) the three modules are called."""
+        return self._project(normalized_x, self._packed_weights(normalized_x), coefficients)
+
+    def _project(self, normalized_x, packed, coefficients):
+        """project_recurrence_inputs on the packed weights `packed` (None: the modules)."""
         finish = self.coefficient_projection if coefficients else (lambda control: control)
-        signature = None
-        if not self.training and not torch.is_grad_enabled():
-            signature = _packing_signature(normalized_x, projections)
-        if signature is None:
+        if packed is None:
             control = F.silu(self.to_control(normalized_x))
             return (self.input_projection(normalized_x), finish(control),
                     self.to_gate(normalized_x))
-        packed = self.__dict__.get("_packed_projection")
-        if packed is None or packed[0] != signature:
-            weight = torch.cat([p.weight for p in projections])
-            bias = torch.cat([p.bias if p.bias is not None else p.weight.new_zeros(p.out_features)
-                              for p in projections])
-            packed = (signature, weight, bias)
-            self.__dict__["_packed_projection"] = packed
-        projected = F.linear(normalized_x, packed[1], packed[2])
+        projections = (self.input_projection, self.to_gate, self.to_control)
+        projected = F.linear(normalized_x, packed["weight"], packed["bias"])
         projected_input, gamma, raw_control = projected.split(
             tuple(p.out_features for p in projections), dim=-1)
         control = F.silu(raw_control)
         return projected_input, finish(control), gamma
 
+    def _packed_weights(self, normalized_x):
+        """The inference weights kept between calls, or None where the modules must be called
+        (see project_recurrence_inputs): the three input projections packed as one matrix, and
+        the same rows regrouped as [signal | gate] and [write | control]."""
+        if self.training or torch.is_grad_enabled():
+            return None
+        projections = (self.input_projection, self.to_gate, self.to_control)
+        signature = _packing_signature(normalized_x, projections)
+        if signature is None:
+            return None
+        packed = self.__dict__.get("_packed_projection")
+        if packed is None or packed["signature"] != signature:
+            weight = torch.cat([p.weight for p in projections])
+            bias = torch.cat([p.bias if p.bias is not None else p.weight.new_zeros(p.out_features)
+                              for p in projections])
+            channels, memory = self.inner, self.memory_dimension
+            gate_rows = slice(channels + memory, 2 * channels + memory)
+            wide = (torch.cat([weight[:channels], weight[gate_rows]]),
+                    torch.cat([bias[:channels], bias[gate_rows]]))
+            narrow = (torch.cat([weight[channels:channels + memory], weight[2 * channels + memory:]]),
+                      torch.cat([bias[channels:channels + memory], bias[2 * channels + memory:]]))
+            packed = {"signature": signature, "weight": weight, "bias": bias, "wide": wide,
+                      "narrow": narrow, "tensors": (weight, bias) + wide + narrow,
+                      "streams": set()}
+            self.__dict__["_packed_projection"] = packed
+        _used_on_this_stream(packed, normalized_x)
+        return packed
+
+    def _padded_coefficient_weights(self, control):
+        """coefficient_projection with its rows padded by zeros to a multiple of 256, kept
+        between calls (rebuilt on the same rules as the packed input weights), or None where the
+        module must be called. The GEMM library runs that many output columns 1.6x faster at
+        d_r = 128 (8,192 rows x 14,528 columns: 114 us, padded to 14,592: 73 us on MI355X); the
+        scan reads the real columns through strided views."""
+        signature = _packing_signature(control, (self.coefficient_projection,))
+        if signature is None:
+            return None
+        padded = self.__dict__.get("_padded_coefficients")
+        if padded is None or padded["signature"] != signature:
+            module = self.coefficient_projection
+            extra = (-module.out_features) % 256
+            weight = torch.cat([module.weight, module.weight.new_zeros(extra, module.in_features)])
+            bias = torch.cat([module.bias, module.bias.new_zeros(extra)])
+            padded = {"signature": signature, "tensors": (weight, bias), "streams": set()}
+            self.__dict__["_padded_coefficients"] = padded
+        _used_on_this_stream(padded, control)
+        return padded["tensors"]
+
+    def _recurrence_inputs(self, normalized_x, coefficients=True):
+        """(signal, raw write, coefficient rows or control, gamma, input projection) for the
+        forward. Inference takes the packed weights: for at least SPLIT_ROWS tokens as two GEMMs,
+        [signal | gate] (2 d_e columns, a multiple of the GEMM tiles at the mixer's widths) and
+        the narrow [write | control] (8,192 tokens at d_e 2048: 123 us against 160 us for the
+        4,288-column GEMM on MI355X), fewer tokens as the one packed GEMM (a decode step is
+        launch-bound); and the coefficient projection on its padded weight, whose output rows
+        are wider than the coefficients by up to 255 zero columns. The input projection is
+        returned whole only where it exists as one tensor (None after the two GEMMs). Below
+        SPLIT_ROWS tokens the modules' own weights serve (decode steps: there the padded
+        coefficient GEMM was slower)."""
+        channels, memory = self.inner, self.memory_dimension
+        packed = self._packed_weights(normalized_x)
+        rows = normalized_x.numel() // max(normalized_x.shape[-1], 1)
+        if packed is None or rows < SPLIT_ROWS:
+            input_projection, finished, gamma = self._project(normalized_x, packed, False)
+            signal, raw_write = input_projection.split((channels, memory), dim=-1)
+            control = finished
+        else:
+            input_projection = None
+            both = F.linear(normalized_x, *packed["wide"])
+            signal, gamma = both.split((channels, channels), dim=-1)
+            narrow = F.linear(normalized_x, *packed["narrow"])
+            raw_write, raw_control = narrow.split((memory, self.coefficient_bottleneck), dim=-1)
+            control = F.silu(raw_control)
+        if not coefficients:
+            return signal, raw_write, control, gamma, input_projection
+        if packed is not None and rows >= SPLIT_ROWS:
+            padded = self._padded_coefficient_weights(control)
+            if padded is not None:
+                return signal, raw_write, F.linear(control, *padded), gamma, input_projection
+        return signal, raw_write, self.coefficient_projection(control), gamma, input_projection
+
     def _forms_coefficients_in_scan(self, normalized_x, cache):
         """Whether this call takes the coefficient-forming scan (model/mira_mixer.py:739-760):
         an uncached, gradient-free forward whose coefficient_projection is a plain, unhooked
-        nn.Linear, and no positive-pole remapping."""
-        return (normalized_x.is_cuda and cache is None and not self.positive_poles
-                and not torch.is_grad_enabled() and _plain_linear(self.coefficient_projection))
+        nn.Linear, no positive-pole remapping, and a geometry the scan has a kernel for (else
+        the forward projects the coefficients itself, on the padded weight)."""
+        if not (normalized_x.is_cuda and cache is None and not self.positive_poles
+                and not torch.is_grad_enabled() and _plain_linear(self.coefficient_projection)):
+            return False
+        batch, tokens, _ = normalized_x.shape
+        return plugin.control_scan_serves(batch, tokens, self.inner, self.order,
+                                          self.memory_dimension, self.coefficient_bottleneck,
+                                          normalized_x.dtype, normalized_x.device.index)
 
     def forward(self, normalized_x, attn_mask=None, cache=None, layer=None):
         if cache is not None and not (prefix_cache.enabled() and layer is not None
@@ -160,9 +257,8 @@ class MiraMixer(nn.Module):
         batch, tokens, _ = normalized_x.shape
         channels, order, memory = self.inner, self.order, self.memory_dimension
         if self._forms_coefficients_in_scan(normalized_x, cache):
-            input_projection, control, gamma = self.project_recurrence_inputs(
+            signal, raw_write, control, gamma, _ = self._recurrence_inputs(
                 normalized_x, coefficients=False)
-            signal, raw_write = input_projection.split((channels, memory), dim=-1)
             valid = None if attn_mask is None else attn_mask[:, -tokens:].bool()
             projection = self.coefficient_projection
             mixed = plugin.matrix_lattice_iir_control(
@@ -178,9 +274,14 @@ class MiraMixer(nn.Module):
         alpha_size = channels * order
         rho_size = channels * (order + 1)
         read_size = (order + 1) * memory
-        input_projection, coefficients, gamma = self.project_recurrence_inputs(normalized_x)
-        signal, raw_write = input_projection.split((channels, memory), dim=-1)
-        raw_alpha, raw_beta, raw_rho, memory_read = coefficients.split(
+        if torch.is_grad_enabled() and cache is None:
+            # training: the module outputs themselves, which the backward fills whole
+            input_projection, coefficients, gamma = self.project_recurrence_inputs(normalized_x)
+            signal, raw_write = input_projection.split((channels, memory), dim=-1)
+        else:
+            signal, raw_write, coefficients, gamma, input_projection = self._recurrence_inputs(
+                normalized_x)
+        raw_alpha, raw_beta, raw_rho, memory_read = coefficients[..., :self.read_span[1]].split(
             (alpha_size, alpha_size, rho_size, read_size), dim=-1)
         if self.positive_poles:
             value = raw_alpha.float()

@@ -70,8 +70,14 @@ def test_graph_replay_equals_eager_steps(torch_mod, parts):
         return hook
 
     eager = generate(model, prompt, 10, on_token=keep("eager"))
+    kept = [block.mixer.__dict__["_packed_projection"]["tensors"] for block in model.blocks]
     replayed = generate(model, prompt, 10, graph=True, on_token=keep("graph"))
     assert torch.equal(eager, replayed)
+    # the packed input weights serve the warm-up's stream and the capture as they are: nothing
+    # is rebuilt, so the captured step holds no weight copies
+    for block, before in zip(model.blocks, kept):
+        after = block.mixer.__dict__["_packed_projection"]["tensors"]
+        assert all(a is b for a, b in zip(after, before))
     assert len(seen["eager"]) == len(seen["graph"]) == 10
     assert all(torch.equal(a, b) for a, b in zip(seen["eager"], seen["graph"]))
     again = generate(model, prompt, 10, graph=True)

@@ -78,6 +78,40 @@ def test_llm_matches_the_oracle(torch_mod, model_cls, dtype, bound):
     assert error <= bound, f"{dtype}: scaled error {error:.3e}"
 
 
+@pytest.mark.parametrize("dtype,bound", [("float32", FP32_SCALED), ("bfloat16", HALF_SCALED)])
+def test_split_and_padded_projections_match_the_oracle(torch_mod, model_cls, monkeypatch, dtype,
+                                                       bound):
+    """The long-input projections -- [signal | gate] and [write | control] as two GEMMs, and
+    the coefficient projection on weights padded to 1,024 rows (d_e 100: 796 coefficients) --
+    against the oracle, with a padding mask."""
+    torch = torch_mod
+    from mira_amd import mixer as mixer_module
+
+    monkeypatch.setattr(mixer_module, "SPLIT_ROWS", 1)
+    cfg = dict(CFG, lattice_d_e=100)
+    torch.manual_seed(3)
+    model = model_cls(**cfg)
+    with torch.no_grad():
+        for name, value in model.named_parameters():
+            if name.endswith("weight") and value.dim() == 2:
+                value.normal_(0.0, 1.0 / np.sqrt(value.shape[1]))
+            elif name.endswith("bias"):
+                value.normal_(0.0, 0.05)
+    model = model.to(device="cuda", dtype=getattr(torch, dtype)).eval()
+    rng = np.random.default_rng(8)
+    ids = rng.integers(0, cfg["vocab_size"], (2, 41))
+    valid = np.ones((2, 41), bool)
+    valid[1, :3] = False
+    with torch.no_grad():
+        got = model(torch.tensor(ids, device="cuda"),
+                    attention_mask=torch.tensor(valid, device="cuda")).logits
+    mixer = model.blocks[0].mixer
+    assert mixer.__dict__["_padded_coefficients"]["tensors"][0].shape[0] == 1024
+    want, _ = St.llm_forward(ids, _params(model), cfg, valid=valid, rnd=_rounding(torch, dtype))
+    error = scaled(got.float().cpu().numpy(), want)
+    assert error <= bound, f"{dtype}: scaled error {error:.3e}"
+
+
 def test_prompt_then_steps_equals_one_shot(torch_mod, model_cls):
     torch = torch_mod
     from mira_amd.prefix_cache import PrefixCache

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from mira_amd import config, hardware, mira, prefix_cache
+from mira_amd import mixer as mixer_module
 from mira_amd.llm import MiraLLM
 from mira_amd.mixer import MiraMixer
 from mira_amd.prefix_cache import PrefixCache, affordable, state_bytes
@@ -170,6 +171,59 @@ def test_packed_projection_respects_hooks_and_subclasses():
     mixer.to_gate = replacement
     with torch.no_grad():
         torch.testing.assert_close(mixer.project_recurrence_inputs(x)[2], base * 2.0)
+
+
+def _module_inputs(mixer, x):
+    """What the forward's projections must equal: the modules called one by one."""
+    channels, memory = mixer.inner, mixer.memory_dimension
+    signal, raw_write = mixer.input_projection(x).split((channels, memory), dim=-1)
+    control = torch.nn.functional.silu(mixer.to_control(x))
+    return signal, raw_write, control, mixer.coefficient_projection(control), mixer.to_gate(x)
+
+
+@pytest.mark.parametrize("split_rows", [1, 10 ** 9])
+def test_forward_projections_match_module_calls(monkeypatch, split_rows):
+    """The forward's inference projections -- [signal | gate] and [write | control] as two
+    GEMMs from SPLIT_ROWS tokens on, the packed GEMM below, and the coefficient projection on
+    its zero-padded weight -- give the module calls' values; the padding columns are zero."""
+    monkeypatch.setattr(mixer_module, "SPLIT_ROWS", split_rows)
+    mixer = _projection_mixer()
+    x = torch.randn(2, 7, 32)
+    with torch.no_grad():
+        signal, raw_write, coefficients, gamma, whole = mixer._recurrence_inputs(x)
+        _, _, control, _, _ = mixer._recurrence_inputs(x, coefficients=False)
+        want = _module_inputs(mixer, x)
+    width = mixer.coefficient_projection.out_features
+    if split_rows == 1:                        # long input: split GEMMs, padded coefficients
+        assert coefficients.shape[-1] % 256 == 0 and coefficients.shape[-1] - width < 256
+        assert torch.count_nonzero(coefficients[..., width:]) == 0
+        assert whole is None
+    else:                                      # short input: the packed GEMM, the module's weight
+        assert coefficients.shape[-1] == width and whole is not None
+    for got, expect in zip((signal, raw_write, control, coefficients[..., :width], gamma), want):
+        torch.testing.assert_close(got, expect, rtol=1e-5, atol=1e-6)
+
+
+def test_padded_coefficients_follow_the_module(monkeypatch):
+    """The padded copy of coefficient_projection is rebuilt when its parameters change, and a
+    hook on the module sends the forward back to calling it."""
+    monkeypatch.setattr(mixer_module, "SPLIT_ROWS", 1)
+    mixer = _projection_mixer()
+    x = torch.randn(1, 3, 32)
+    width = mixer.coefficient_projection.out_features
+    with torch.no_grad():
+        before = mixer._recurrence_inputs(x)[2][..., :width]
+        mixer.coefficient_projection.weight.mul_(0.5)
+        after = mixer._recurrence_inputs(x)[2][..., :width]
+        assert not torch.equal(before, after)
+        torch.testing.assert_close(after, _module_inputs(mixer, x)[3], rtol=1e-5, atol=1e-6)
+        handle = mixer.coefficient_projection.register_forward_hook(lambda m, a, out: out * 2.0)
+        try:
+            hooked = mixer._recurrence_inputs(x)[2]
+        finally:
+            handle.remove()
+    assert hooked.shape[-1] == width
+    torch.testing.assert_close(hooked, 2.0 * after, rtol=1e-5, atol=1e-6)
 
 
 def test_packed_projection_rebuilds_on_parameter_change():
