@@ -210,6 +210,17 @@ int mira_gla_chunked(const void *q, const void *k, const void *v, const float *g
 int mira_gla_step(const void *q, const void *k, const void *v, const float *g, float *S,
                   void *o, int B, int H, int dk, int dv, int dtype, void *stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * The MiraBlock feed-forward's first projection and activation (model/mira_block.py:38-48,
+ * down(SiLU(up(x)))): out[rows, out_features] = SiLU(x W^T + bias), bf16 in and out, as one
+ * hipBLASLt GEMM whose epilogue adds the bias and applies SiLU before the single rounding.
+ * x [rows, in_features], weight [out_features, in_features] (nn.Linear's layout), bias
+ * [out_features], out [rows, out_features], all contiguous bf16. MIRA_DECLINE when hipBLASLt
+ * offers no algorithm for the shape. The first call per shape and device sets up a plan (and
+ * the first call per device a 32 MiB workspace); it is not for graph capture. */
+int mira_linear_silu(const void *x, const void *weight, const void *bias, void *out,
+                     long long rows, int in_features, int out_features, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,7 +63,8 @@ def build(jobs=None, verbose=True):
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         objects = list(pool.map(lambda s: compile_one(s, objdir, digest), srcs))
     tmp = LIBRARY + ".tmp"
-    command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", tmp]
+    command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-lhipblaslt",
+               "-o", tmp]
     result = subprocess.run(command, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stdout}\n{result.stderr}")

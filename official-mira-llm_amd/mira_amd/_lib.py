@@ -54,6 +54,7 @@ SIGNATURES = {
     "mira_gla_workspace_bytes": ([i32, i32, i32, i32, i32], sz),
     "mira_gla_chunked": ([p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, p, sz, p], i32),
     "mira_gla_step": ([p, p, p, p, p, p, i32, i32, i32, i32, i32, p], i32),
+    "mira_linear_silu": ([p, p, p, p, i64, i32, i32, p], i32),
 }
 
 

@@ -3,7 +3,9 @@ RMSNorm -> feed-forward on the residual stream (model/mira_block.py:156-205).
 
 The constructor and forward keep the reference's signatures, so a MiraLLM assembled from these
 blocks is called as the reference's is. The mixer is mira_amd.mixer.MiraMixer, whose scan runs on
-the HIP library; the norms and the feed-forward are PyTorch (their GEMMs go to hipBLASLt).
+the HIP library; the norms and the feed-forward are PyTorch (their GEMMs go to hipBLASLt), except
+that in inference the feed-forward's up projection, bias and SiLU run as one GEMM of the library
+(mira_amd.mira.linear_silu).
 Mixture-of-experts feed-forwards (model/mira_block.py:51-145) are not part of the scan's hot path
 and are not built: a `moe` argument raises.
 """
@@ -15,7 +17,14 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .mixer import MiraMixer
+from . import mira as plugin
+from .mixer import MiraMixer, _plain_linear
+
+
+def _global_hooks():
+    from torch.nn.modules import module as module_globals
+
+    return bool(module_globals._global_forward_pre_hooks or module_globals._global_forward_hooks)
 
 
 class RMSNorm(nn.Module):
@@ -54,7 +63,23 @@ class FeedForward(nn.Module):
         self.dropout = nn.Dropout(dropout)
 
     def forward(self, x):
-        return self.dropout(self.down(F.silu(self.up(x))))
+        hidden = None
+        if self._fused(x):
+            # inference on the GPU: the up projection with bias and SiLU as one GEMM
+            hidden = plugin.linear_silu(x, self.up.weight, self.up.bias)
+        if hidden is None:
+            hidden = F.silu(self.up(x))
+        return self.dropout(self.down(hidden))
+
+    def _fused(self, x):
+        """The fused up projection serves this call: no gradients, bf16 on the GPU, a plain
+        unhooked nn.Linear with a bias, rows that fit, and the HIP library loaded."""
+        up = self.up
+        return (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16
+                and type(x) is torch.Tensor and up.bias is not None
+                and up.weight.dtype == torch.bfloat16 and _plain_linear(up)
+                and not _global_hooks() and x.numel() // max(x.shape[-1], 1) < 2 ** 31
+                and plugin.status(x.device.index)[0])
 
 
 class MiraBlock(nn.Module):

@@ -48,7 +48,8 @@ ARCH_STAGE = {"cauchy_x_mobius": 3, "cauchy_x_hyperbolic": 6, "cauchy_x_identity
 DTYPE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 CONV_WIDTH = 4
 GLA_DIM = 128
-USED = {"forward": 0, "backward": 0, "step": 0, "control": 0, "diag": 0, "gla": 0}
+USED = {"forward": 0, "backward": 0, "step": 0, "control": 0, "diag": 0, "gla": 0,
+        "linear_silu": 0}
 REPORTED = set()
 _WORKSPACES = {}
 _WORKSPACE_LOCK = threading.Lock()      # autograd / DataParallel threads may launch
@@ -692,3 +693,28 @@ def gla_step(q, k, v, g, state, out=None):
         return None
     USED["step"] += 1
     return o
+
+
+def linear_silu(x, weight, bias):
+    """SiLU(x W^T + b) of the MiraBlock feed-forward's first projection (model/mira_block.py:
+    38-48) as one hipBLASLt GEMM with a bias + SiLU epilogue (mira_linear_silu): bf16 x [..., in],
+    weight [out, in], bias [out], all contiguous, on one GPU. None where the library declines
+    (no algorithm for the shape); ValueError for arguments it cannot take."""
+    tensors = (x, weight, bias)
+    if any(t.dtype != torch.bfloat16 or not t.is_cuda for t in tensors):
+        raise ValueError("linear_silu: x, weight and bias must be bf16 tensors on the GPU")
+    if len({t.device for t in tensors}) != 1:
+        raise ValueError("linear_silu: x, weight and bias must be on one device")
+    if weight.dim() != 2 or bias.shape != (weight.shape[0],) or x.shape[-1] != weight.shape[1]:
+        raise ValueError("linear_silu: shapes must be x [..., in], weight [out, in], bias [out]")
+    x = x.contiguous()
+    weight, bias = weight.contiguous(), bias.contiguous()
+    rows = x.numel() // x.shape[-1]
+    out = torch.empty(*x.shape[:-1], weight.shape[0], device=x.device, dtype=x.dtype)
+    lib = _lib.require()
+    code = lib.mira_linear_silu(_ptr(x), _ptr(weight), _ptr(bias), _ptr(out), rows,
+                                int(weight.shape[1]), int(weight.shape[0]), _stream(x.device))
+    if _lib.check(code, "mira_linear_silu") is None:
+        return None
+    USED["linear_silu"] += 1
+    return out

@@ -112,6 +112,30 @@ def test_split_and_padded_projections_match_the_oracle(torch_mod, model_cls, mon
     assert error <= bound, f"{dtype}: scaled error {error:.3e}"
 
 
+@pytest.mark.parametrize("rows,width,hidden", [(37, 64, 160), (8192, 2048, 8192)])
+def test_fused_feed_forward_projection(torch_mod, model_cls, rows, width, hidden):
+    """The inference feed-forward's up projection, bias and SiLU as one GEMM (mira_linear_silu)
+    against the unfused torch steps, at a small shape and the cfg5 one (bf16: one rounding
+    against two, so a few outputs land one bf16 ulp away)."""
+    torch = torch_mod
+    from mira_amd import mira
+    from mira_amd.block import FeedForward
+
+    torch.manual_seed(4)
+    ffn = FeedForward(width, hidden=hidden).to(device="cuda", dtype=torch.bfloat16).eval()
+    x = torch.randn(1, rows, width, device="cuda", dtype=torch.bfloat16)
+    before = mira.USED["linear_silu"]
+    with torch.no_grad():
+        fused = mira.linear_silu(x, ffn.up.weight, ffn.up.bias)
+        steps = torch.nn.functional.silu(ffn.up(x))
+        whole = ffn(x)
+    assert mira.USED["linear_silu"] == before + 2
+    assert fused.shape == steps.shape
+    error = scaled(fused.float().cpu().numpy(), steps.float().cpu().numpy())
+    assert error <= 1e-2, f"fused SiLU(up): scaled error {error:.3e}"
+    torch.testing.assert_close(whole, ffn.down(fused), rtol=0, atol=0)
+
+
 def test_prompt_then_steps_equals_one_shot(torch_mod, model_cls):
     torch = torch_mod
     from mira_amd.prefix_cache import PrefixCache
