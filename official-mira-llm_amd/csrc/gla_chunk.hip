@@ -41,7 +41,10 @@ constexpr int DK = 128, DV = 128;  // head dims
 constexpr int VB = 32;             // value columns per workgroup
 constexpr int BLOCKS = DV / VB;    // workgroups per head
 constexpr int THREADS = 512;       // 8 waves
-constexpr int VS = VB + 8;         // LDS row (halfwords) of a value tile
+// LDS row (halfwords) of a value tile, unpadded: its only reads are the transposing loads, whose
+// 16-lane groups then cover the 64 banks once (a row of 16 dwords: 4 rows x 4 lanes x 2 dwords,
+// the group's second half 8 dwords on); a padded row (20 dwords) put 2 lanes on a bank
+constexpr int VS = VB;
 constexpr int QS = DK + 8;         // LDS row (halfwords) of a feature-contiguous tile
 constexpr int OS = VB + 8;         // LDS row (halfwords) of the output staging tile
 constexpr unsigned OUT_OF_RANGE = 0x80000000u;
