@@ -701,6 +701,116 @@ def cpu_leg(tokens=8192, channels=2048, runs=3):
             "host_cpus": os.cpu_count(), "numpy": np.__version__, "torch": torch.__version__}
 
 
+def _cpu_gla_sample(streams, tokens, seed):
+    """The reference CPU mixer's per-token loop in its GLA realisation (the K = 1 lattice with
+    C = d_v = M = d_k = 128 per (b, head) stream; the oracle's restatement, numpy float32) on
+    `streams` streams of the cfg3 inputs for `tokens` tokens. Inputs are drawn first; returns
+    the compute seconds."""
+    import numpy as np
+
+    from oracle import baseline as Bl
+
+    rng = np.random.default_rng(seed)
+    q, k, v, g = Bl.gla_inputs(rng, 1, tokens, streams, 128, 128)
+    S0 = (rng.standard_normal((1, streams, 128, 128)) * 0.1).astype(np.float32)
+    t0 = time.perf_counter()
+    Bl.gla_recurrent(q, k, v, g, S0, dtype=np.float32)
+    return time.perf_counter() - t0
+
+
+def _cpu_decode_sample(heads, channels, steps, seed):
+    """`steps` cfg4 decode steps on the CPU (the oracle's restatement, numpy float32): the GLA
+    state update and readout of `heads` (b, head) streams and the conv + diagonal step of
+    `channels` (b, d) channels, each step from the previous one's states. Returns seconds."""
+    import numpy as np
+
+    from oracle import baseline as Bl
+
+    rng = np.random.default_rng(seed)
+    q, k, v, g = Bl.gla_inputs(rng, 1, steps, heads, 128, 128)
+    S = (rng.standard_normal((1, heads, 128, 128)) * 0.1).astype(np.float32)
+    x, a, w, bias, h = Bl.diag_inputs(rng, 1, steps, channels, h0_scale=0.1)
+    ring = (rng.standard_normal((1, channels, 3)) * 0.1).astype(np.float32)
+    t0 = time.perf_counter()
+    for t in range(steps):
+        _, S = Bl.gla_recurrent(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], g[:, t:t + 1], S,
+                                dtype=np.float32)
+        _, h, ring = Bl.diag_conv_scan(x[:, t:t + 1], a[:, t:t + 1], w, bias, h, ring, pos=3 + t,
+                                       dtype=np.float32)
+    return time.perf_counter() - t0
+
+
+def _cpu_job(job):
+    from threadpoolctl import threadpool_limits
+
+    kind, rest = job
+    with threadpool_limits(limits=1):
+        return (_cpu_gla_sample if kind == "gla" else _cpu_decode_sample)(*rest)
+
+
+def _cpu_split(kind, jobs, runs):
+    """Median over `runs` of the slowest worker's seconds, one fresh spawned worker per job."""
+    import multiprocessing
+    import statistics
+
+    with multiprocessing.get_context("spawn").Pool(len(jobs)) as pool:
+        pool.map(_cpu_job, [(kind, jobs[0][:-1] + (99,))] * len(jobs))     # warm-up
+        return statistics.median(max(pool.map(_cpu_job, [(kind, j[:-1] + (j[-1] + 100 * r,))
+                                                          for j in jobs]))
+                                 for r in range(runs))
+
+
+def cpu_gla_leg(tokens=2048, runs=3):
+    """cfg3's CPU baseline on a fixed prefix (SURVEY's rule for the long configs: the cost per
+    token is constant, so the rate extrapolates): all 64 (b, head) streams for `tokens` tokens,
+    one warm-up, median of `runs`, on one thread and on all the job's cores (4 streams each)."""
+    import statistics
+
+    from threadpoolctl import threadpool_limits
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    with threadpool_limits(limits=1):
+        _cpu_gla_sample(64, 16, 99)
+        single = statistics.median(_cpu_gla_sample(64, tokens, seed) for seed in range(runs))
+    per = 64 // cores
+    parallel = _cpu_split("gla", [(per, tokens, i) for i in range(cores)], runs)
+    # the GPU rate counts (b, t) tokens of all 16 heads: 4 sequences of `tokens` tokens
+    return {"value": 4 * tokens / parallel, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"the first {tokens} of 8192 tokens of cfg3 (B 4 x H 16 = 64 streams, "
+                      f"d_k = d_v = 128), the reference CPU per-token loop in its GLA "
+                      f"realisation (oracle gla_recurrent, numpy float32): {cores} worker "
+                      f"processes of {per} streams, one warm-up, median of {runs} "
+                      f"({parallel:.2f} s)",
+            "single_thread": {"value": 4 * tokens / single, "unit": "tokens/s", "cores": 1,
+                              "seconds": round(single, 2)}}
+
+
+def cpu_decode_leg(steps=4, runs=3):
+    """cfg4's CPU baseline on a fixed number of steps: the batch-256 decode step (GLA over
+    256 x 16 streams, conv + diagonal over 256 x 2048 channels), one warm-up, median of `runs`,
+    on one thread and on all the job's cores (an equal share of streams and channels each)."""
+    import statistics
+
+    from threadpoolctl import threadpool_limits
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    heads, channels = 256 * 16, 256 * 2048
+    with threadpool_limits(limits=1):
+        _cpu_decode_sample(64, 1024, 1, 99)
+        single = statistics.median(_cpu_decode_sample(heads, channels, steps, seed)
+                                   for seed in range(runs))
+    parallel = _cpu_split("decode", [(heads // cores, channels // cores, steps, i)
+                                     for i in range(cores)], runs)
+    return {"value": steps / parallel, "unit": "steps/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} cfg4 decode steps at batch 256 (GLA state [256,16,128,128] and "
+                      f"conv + diagonal over [256,2048], oracle restatement, numpy float32): "
+                      f"{cores} worker processes of {heads // cores} streams and "
+                      f"{channels // cores} channels, one warm-up, median of {runs} "
+                      f"({parallel:.2f} s)",
+            "single_thread": {"value": steps / single, "unit": "steps/s", "cores": 1,
+                              "seconds": round(single, 2)}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -857,6 +967,10 @@ def main():
                                                    "64-token prompt, tokens/s per batch size")}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_leg()
+        if "matrix_state_prefill" in line:
+            line["matrix_state_prefill"]["cpu_baseline"] = cpu_gla_leg()
+        if "decode" in line:
+            line["decode"]["cpu_baseline"] = cpu_decode_leg()
     if args.calibrate:
         calibrate(torch, 5)
     print(json.dumps(line), flush=True)
