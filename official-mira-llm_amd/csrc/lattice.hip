@@ -583,62 +583,96 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
 // One token moves the whole [B,K,C,M] float32 state through HBM once each way, so the step is a
 // stream: a block takes one sequence b and 256 / (M/8) channels, a lane owns 8 consecutive memory
 // slots of one channel (two 16-byte accesses per state row), s and nu of the sequence are staged
-// in LDS once, and the stage maps run once per channel. The update and readout are the replay's
-// (stage K's level read out through sum V^(K-1) nu_K and sum s nu_K). A masked token copies the
-// state and writes 0.
+// in LDS once, and the stage maps run once per channel (see the kernel for the load order that
+// keeps the state loads in flight meanwhile). The update and readout are the replay's (stage
+// K's level read out through sum V^(K-1) nu_K and sum s nu_K). A masked token copies the state
+// and writes 0.
 __host__ __device__ constexpr bool step_kernel_serves(int K, int M) { return K <= 4 && M >= 8 && M <= 128; }
 
-template <typename IO, int K, int M>
-__global__ __launch_bounds__(BLOCK) void lattice_step_kernel(LatticeArgs a) {
+template <typename IO, int K, int M, bool HAS_STATE, int SB>
+__global__ __launch_bounds__(SB) void lattice_step_kernel(LatticeArgs a) {
     constexpr int LPC = M / 8;                   // lanes of a channel
-    constexpr int CPB = BLOCK / LPC;             // channels of a block
+    constexpr int CPB = SB / LPC;             // channels of a block
     constexpr int NC = coef_count(K, true);
+    constexpr int SPT = ((K + 2) * M + SB - 1) / SB;   // s / nu values a thread stages
+    static_assert(CPB <= SB, "one staging thread per channel");
     const int groups = (a.C + CPB - 1) / CPB;
     const int b = blockIdx.x / groups, c0 = (blockIdx.x % groups) * CPB;
     const int tid = threadIdx.x, cl = tid / LPC, part = tid % LPC, c = c0 + cl;
     __shared__ __align__(16) float s_sn[(K + 2) * M];     // s, then nu_0 .. nu_K
     __shared__ float s_coef[NC * CPB];                     // [quantity][channel]
+    // Load order: the small operands (s and nu of the sequence, and thread i < CPB's channel's
+    // coefficients, kept raw) are issued first, then the state (the step's HBM traffic). Loads
+    // complete in issue order, so forming the stage maps and filling LDS waits only for the small
+    // ones while the state loads stay in flight, also across the barrier (which fences LDS only).
+    // Every load below runs in every thread (indices clamped into range, results of the clamped
+    // ones unused): loads under divergent branches would be waited for at the branch's end.
     const IO *write = static_cast<const IO *>(a.write);
     const IO *read = static_cast<const IO *>(a.read);
-    for (int i = tid; i < (K + 2) * M; i += BLOCK)
-        s_sn[i] = i < M ? load(write + (long long)b * M + i)
-                        : load(read + (long long)b * a.read_row + (i - M));
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
-    for (int i = tid; i < CPB && c0 + i < a.C; i += BLOCK) {
-        const int ch = c0 + i;
-        const IO *alpha = static_cast<const IO *>(a.alpha) + (long long)b * a.alpha_row + (long long)ch * K;
-        const IO *beta = static_cast<const IO *>(a.beta) + (long long)b * a.beta_row + (long long)ch * K;
-        const IO *rho = static_cast<const IO *>(a.rho) + (long long)b * a.rho_row + (long long)ch * (K + 1);
+    IO sn[SPT];
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+        const int i = min(tid + j * SB, (K + 2) * M - 1);
+        sn[j] = i < M ? write[(long long)b * M + i] : read[(long long)b * a.read_row + (i - M)];
+    }
+    const bool stager = tid < CPB && c0 + tid < a.C;
+    const int ch = min(c0 + tid, a.C - 1);
+    const IO *alpha = static_cast<const IO *>(a.alpha) + (long long)b * a.alpha_row + (long long)ch * K;
+    const IO *beta = static_cast<const IO *>(a.beta) + (long long)b * a.beta_row + (long long)ch * K;
+    const IO *rho = static_cast<const IO *>(a.rho) + (long long)b * a.rho_row + (long long)ch * (K + 1);
+    IO araw[K], braw[K], rraw[K + 1];
+#pragma unroll
+    for (int k = 0; k < K; ++k) { araw[k] = alpha[k]; braw[k] = beta[k]; }
+#pragma unroll
+    for (int k = 0; k <= K; ++k) rraw[k] = rho[k];
+    const IO xraw = static_cast<const IO *>(a.x)[(long long)b * a.x_row + ch];
+    const IO graw = static_cast<const IO *>(a.gamma)[(long long)b * a.gamma_row + ch];
+    // the flag's load without a branch (a dummy address without a mask), so nothing waits on it
+    const uint8_t flag = *(a.valid ? a.valid + b : static_cast<const uint8_t *>(a.write));
+    __builtin_amdgcn_sched_barrier(0);           // the small loads stay ahead of the state's
+    float V[K][8];
+    if constexpr (HAS_STATE) {
+        const int cs = min(c, a.C - 1);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            float rc, rs;
-            stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc, rs);
-            s_coef[k * CPB + i] = rc;
-            s_coef[(K + k) * CPB + i] = rs;
-        }
-        s_coef[2 * K * CPB + i] = load(static_cast<const IO *>(a.x) + (long long)b * a.x_row + ch);
-#pragma unroll
-        for (int k = 0; k <= K; ++k) s_coef[(2 * K + 1 + k) * CPB + i] = load(rho + k);
-        s_coef[(3 * K + 2) * CPB + i] =
-            silu(load(static_cast<const IO *>(a.gamma) + (long long)b * a.gamma_row + ch));
-    }
-    __syncthreads();
-    if (c >= a.C) return;                        // whole channel groups; no barrier follows
-    const bool valid = a.valid ? a.valid[b] != 0 : true;
-    float V[K][8];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        if (a.state_in) {
             const float4 *src = reinterpret_cast<const float4 *>(
-                a.state_in + (((long long)b * K + k) * a.C + c) * M + part * 8);
+                a.state_in + (((long long)b * K + k) * a.C + cs) * M + part * 8);
             const float4 lo = src[0], hi = src[1];
             V[k][0] = lo.x; V[k][1] = lo.y; V[k][2] = lo.z; V[k][3] = lo.w;
             V[k][4] = hi.x; V[k][5] = hi.y; V[k][6] = hi.z; V[k][7] = hi.w;
-        } else {
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
 #pragma unroll
             for (int e = 0; e < 8; ++e) V[k][e] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+        if (tid + j * SB < (K + 2) * M) s_sn[tid + j * SB] = to_float(sn[j]);
+    // the maps in the waves that hold staging threads (a wave-uniform branch), every lane of them
+    // (those past the block's channels on a clamped one), stored by the staging threads
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) * 64 < CPB) {
+        const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+        float coef[NC];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            stage_coefficients(to_float(araw[k]), to_float(braw[k]), radius_kind, rotation_kind,
+                               coef[k], coef[K + k]);
+        coef[2 * K] = to_float(xraw);
+#pragma unroll
+        for (int k = 0; k <= K; ++k) coef[2 * K + 1 + k] = to_float(rraw[k]);
+        coef[3 * K + 2] = silu(to_float(graw));
+        if (stager) {
+#pragma unroll
+            for (int q = 0; q < NC; ++q) s_coef[q * CPB + tid] = coef[q];
         }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (c >= a.C) return;                        // whole channel groups; no barrier follows
+    const bool valid = a.valid ? flag != 0 : true;
     float y = 0.0f;
     if (valid) {
         float rc[K], rs[K];
@@ -739,7 +773,12 @@ int launch_typed(LatticeArgs &a, hipStream_t stream) {
         if (a.T == 1 && a.chunks == 1 && aligned16(a.state_in) && aligned16(a.state_out)) {
             constexpr int CPB = BLOCK / (M / 8);
             const long long blocks = (long long)a.B * ((a.C + CPB - 1) / CPB);
-            hipLaunchKernelGGL((lattice_step_kernel<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+            if (a.state_in)
+                hipLaunchKernelGGL((lattice_step_kernel<IO, K, M, true, BLOCK>), dim3(blocks), dim3(BLOCK), 0,
+                                   stream, a);
+            else
+                hipLaunchKernelGGL((lattice_step_kernel<IO, K, M, false, BLOCK>), dim3(blocks), dim3(BLOCK), 0,
+                                   stream, a);
             return check_launch("lattice_step_kernel");
         }
     }
