@@ -616,7 +616,7 @@ __global__ __launch_bounds__(SB) void lattice_step_kernel(LatticeArgs a) {
         sn[j] = i < M ? write[(long long)b * M + i] : read[(long long)b * a.read_row + (i - M)];
     }
     const bool stager = tid < CPB && c0 + tid < a.C;
-    const int ch = min(c0 + tid, a.C - 1);
+    const int ch = min(c0 + min(tid, CPB - 1), a.C - 1);    // the block's own channels only
     const IO *alpha = static_cast<const IO *>(a.alpha) + (long long)b * a.alpha_row + (long long)ch * K;
     const IO *beta = static_cast<const IO *>(a.beta) + (long long)b * a.beta_row + (long long)ch * K;
     const IO *rho = static_cast<const IO *>(a.rho) + (long long)b * a.rho_row + (long long)ch * (K + 1);
