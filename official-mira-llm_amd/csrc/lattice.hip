@@ -17,7 +17,9 @@
 //            the last chunk stores the final state. With one chunk this is the whole scan, and at
 //            T = 1 it is the decode step. Stage K's level is never kept, so the replay reads it
 //            out as rc_K sum_m V^(K-1) nu_K + rs_K x sum_m s nu_K instead of forming it per m:
-//            5K - 1 operations per (t, c, m) instead of 5K + 2.
+//            5K - 1 operations per (t, c, m) instead of 5K + 2. At K <= 2, with a channel on
+//            several lanes, the state rows are kept divided by per-channel scales that make every
+//            update output one fused multiply-add (lattice_token_scaled): 3K + 1 operations.
 // A block is 256 threads = G channels x L lanes; lane l of a channel owns M/L memory slots, so a
 // channel's K x M state lives in registers. Per tile of TT tokens the block stages in LDS the
 // write and read vectors s, nu (per (b, t), shared by every channel) and, per (token, channel),
@@ -47,7 +49,8 @@ __host__ __device__ constexpr int tile_for(int K, int M) {
 // channel, not once per lane), x, and for the readout rho and the gate; per token the valid flag.
 // Layout coef[token][quantity][channel] so that a wave's reads of one quantity are contiguous.
 // MODE is the stage mode when the kernel is built for one stage map, 0 when it reads a.mode.
-template <typename IO, int K, bool READOUT, int MODE = 0>
+// SCALED stages the scaled token's quantities (stage_scaled_coefficients) instead.
+template <typename IO, int K, bool READOUT, int MODE = 0, bool SCALED = false>
 __device__ __forceinline__ void stage_coefficient_tile(const LatticeArgs &a, int b, int tile, int n,
                                                        int c0, int G, float *coef,
                                                        unsigned char *valid) {
@@ -61,6 +64,19 @@ __device__ __forceinline__ void stage_coefficient_tile(const LatticeArgs &a, int
         const long long row = (long long)b * a.T + tile + tt;
         const IO *alpha = static_cast<const IO *>(a.alpha) + row * a.alpha_row + (long long)c * K;
         const IO *beta = static_cast<const IO *>(a.beta) + row * a.beta_row + (long long)c * K;
+        if constexpr (SCALED) {
+            float rc[K], rs[K], rho_v[K + 1];
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+                stage_coefficients(load(alpha + k), load(beta + k), radius_kind, rotation_kind, rc[k], rs[k]);
+            const IO *rho = static_cast<const IO *>(a.rho) + row * a.rho_row + (long long)c * (K + 1);
+#pragma unroll
+            for (int k = 0; k <= K; ++k) rho_v[k] = load(rho + k);
+            stage_scaled_coefficients<K>(
+                dst, G, rc, rs, load(static_cast<const IO *>(a.x) + row * a.x_row + c), rho_v,
+                silu(load(static_cast<const IO *>(a.gamma) + row * a.gamma_row + c)));
+            continue;
+        }
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             float rc, rs;
@@ -504,6 +520,11 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     constexpr int MV = M / L;
     constexpr int TT = tile_for(K, M);
     constexpr int NC = coef_count(K, true);
+    // K <= 2 runs the scaled token (one fused multiply-add per update output) where a channel
+    // spans several lanes; a channel on one lane (K d_m <= 32) would hold the unrolled tile's
+    // s and nu of every token in registers and keeps the direct form
+    constexpr bool SCALED = K <= 2 && L > 1;
+    static_assert(!SCALED || scaled_coef_count(K) <= NC, "scaled coefficients fit the staged tile");
     const int groups = (a.C + G - 1) / G;
     int block = blockIdx.x;
     const int group = block % groups;
@@ -537,6 +558,9 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
         }
     const int first = chunk_index * a.chunk;
     const int last = min(first + a.chunk, a.T);
+    float sigma[K];                                            // the channel's scales (SCALED)
+#pragma unroll
+    for (int k = 0; k < K; ++k) sigma[k] = 1.0f;
     const IO *write = static_cast<const IO *>(a.write);
     const IO *read = static_cast<const IO *>(a.read);
     IO *out = static_cast<IO *>(a.out);
@@ -549,15 +573,39 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
             const int tt = i / ((K + 1) * M), rest = i % ((K + 1) * M);
             s_read[i] = load(read + ((long long)b * a.T + tile + tt) * a.read_row + rest);
         }
-        stage_coefficient_tile<IO, K, true, MODE>(a, b, tile, n, group * G, G, s_coef, s_valid);
+        stage_coefficient_tile<IO, K, true, MODE, SCALED>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
-        if (active) {
+        // a full tile of live tokens runs unrolled without branches: the update's outputs then
+        // rotate through registers instead of being copied back every token
+        bool full = SCALED && n == TT;
+        for (int tt = 0; tt < TT && full; ++tt) full = s_valid[tt] != 0;
+        if (active && full) {
+            if constexpr (SCALED) {
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt) {
+                    const float *cf = s_coef + tt * NC * G + cl;
+                    const float y = lattice_token_scaled<K, M, L>(
+                        V, sigma, [&](int q) { return cf[q * G]; }, s_write + tt * M,
+                        s_read + tt * (K + 1) * M, lane);
+                    // the scales back into the state at the tile's end and where one runs small
+                    if (tt == TT - 1 || scales_small(sigma)) scaled_renormalise(V, sigma);
+                    if (lane == 0) s_out[tt * G + cl] = y;
+                }
+            }
+        } else if (active) {
             for (int tt = 0; tt < n; ++tt) {
                 float y = 0.0f;
+                const float *cf = s_coef + tt * NC * G + cl;
                 if (s_valid[tt]) {
-                    const float *cf = s_coef + tt * NC * G + cl;
-                    y = lattice_token<K, M, L>(V, [&](int q) { return cf[q * G]; },
-                                               s_write + tt * M, s_read + tt * (K + 1) * M, lane);
+                    if constexpr (SCALED)
+                        y = lattice_token_scaled<K, M, L>(V, sigma, [&](int q) { return cf[q * G]; },
+                                                          s_write + tt * M, s_read + tt * (K + 1) * M, lane);
+                    else
+                        y = lattice_token<K, M, L>(V, [&](int q) { return cf[q * G]; },
+                                                   s_write + tt * M, s_read + tt * (K + 1) * M, lane);
+                }
+                if constexpr (SCALED) {
+                    if (tt == n - 1 || scales_small(sigma)) scaled_renormalise(V, sigma);
                 }
                 if (lane == 0) s_out[tt * G + cl] = y;
             }
