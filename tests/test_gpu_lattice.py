@@ -153,6 +153,34 @@ def test_per_map_kernels_every_shape(torch_mod, plugin, arch, order, memory):
     assert max_abs(final, want_state) <= 1e-4, f"state: {max_abs(final, want_state):.3e}"
 
 
+@pytest.mark.parametrize("order,memory", [(1, 64), (2, 32), (2, 64), (2, 128)])
+@pytest.mark.parametrize("arch", ["cauchy_x_hyperbolic", "cauchy_x_mobius", "cauchy_x_identity"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_scaled_replay_special_coefficients(torch_mod, plugin, arch, order, memory, dtype):
+    """The replay keeps K <= 2 state rows divided by per-channel scales built from the stage
+    coefficients: exact zeros (alpha = 0 gives sin = 0 or, for the Moebius map, cos = 0), tiny
+    radii (|beta| ~ 1e3 gives r ~ 1e-6), whole stretches of zeros (a zero-initialised
+    projection), masked tokens and partial tiles must all match the fp64 oracle."""
+    rng = np.random.default_rng(300 + 10 * order + memory)
+    B, T, C = 2, 100, 24
+    values = L.random_inputs(rng, B, T, C, order, memory)
+    alpha, beta = values[1], values[6]
+    alpha[rng.random(alpha.shape) < 0.25] = 0.0
+    alpha[0, 40:72] = 0.0                       # every stage of every channel, 32 tokens
+    beta[rng.random(beta.shape) < 0.05] = 1000.0
+    beta[1, 10:14, :5] = -3000.0
+    state = (rng.standard_normal((B, order, C, memory)) * 0.1).astype(np.float32)
+    valid = rng.random((B, T)) > 0.1
+    valid[0, 40:72] = True
+    for chunk in (48, None):
+        y, final = _run(plugin, torch_mod, values, valid, state, arch, dtype, chunk=chunk)
+        want_y, want_state = _oracle(values, valid, state, arch, dtype, torch_mod)
+        _assert(y, want_y, dtype, f"{arch} K{order} d_m{memory} chunk {chunk} output")
+        assert max_abs(final, want_state) <= (FP32_ABS if dtype == "float32" else 1e-4), \
+            f"state: {max_abs(final, want_state):.3e}"
+        assert np.isfinite(y).all() and np.isfinite(final).all()
+
+
 @pytest.mark.parametrize("chunk", [1, 5, 16, 17, 64, None, 1000])
 def test_chunking_is_invisible(torch_mod, plugin, chunk):
     rng = np.random.default_rng(11)
