@@ -216,12 +216,18 @@ __device__ __forceinline__ bf16x8 operand(const uint16_t *p) {
 }
 __device__ __forceinline__ uint16_t to_bf16(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
 __device__ __forceinline__ float from_bf16(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-// lane i of a 16-lane row takes lane i + N's value; past the row's end it keeps `fill`
+// lane i of a 16-lane row takes lane i + N's value; past the row's end it keeps `fill` (a zero
+// fill is the DPP's own bound-zero mode, which needs no register holding the fill)
 template <int N>
 __device__ __forceinline__ float from_row_above(float v, float fill) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill),
                                                                  __builtin_bit_cast(int, v),
                                                                  0x100 + N, 0xf, 0xf, false));
+}
+template <int N>
+__device__ __forceinline__ float from_row_above_or_zero(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 0x100 + N, 0xf, 0xf, true));
 }
 // X_t <- X_(t+N) X_t across the row (identity past its end): one round of the suffix scan
 template <int N, int K>
@@ -230,7 +236,8 @@ __device__ __forceinline__ void suffix_round(float (&X)[K][K]) {
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int j = 0; j < K; ++j) Y[k][j] = from_row_above<N>(X[k][j], k == j ? 1.0f : 0.0f);
+        for (int j = 0; j < K; ++j)
+            Y[k][j] = k == j ? from_row_above<N>(X[k][j], 1.0f) : from_row_above_or_zero<N>(X[k][j]);
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
@@ -370,7 +377,8 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
                 float v = 0.0f;
 #pragma unroll
                 for (int j = 0; j < K; ++j)
-                    v = fmaf(from_row_above<1>(X[k][j], k == j ? 1.0f : 0.0f), bx[j], v);
+                    v = fmaf(k == j ? from_row_above<1>(X[k][j], 1.0f) : from_row_above_or_zero<1>(X[k][j]),
+                             bx[j], v);
                 zb[k] = v;
             }
 #pragma unroll
@@ -413,7 +421,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_summary_mfma(LatticeArgs a) {
 #pragma unroll
         for (int q = 0; q < PER_WAVE; ++q) {
             const int tl = wave + 4 * q;
-            if (tl < TILES) {
+            if (TILES % 4 == 0 || tl < TILES) {
                 const int rt = tl % 2, ct = tl / 2;
                 const int kk = 8 * (lane >> 5);
                 const bf16x8 B = operand(&s_wT[32 * ct + (lane & 31)][kk]);

@@ -48,7 +48,8 @@ __device__ __forceinline__ float load(const IO *p) { return to_float(*p); }
 // 3 cauchy_x_mobius, 6 cauchy_x_hyperbolic, 7 cauchy_x_identity, then for 8..19 radius
 // (mode-8)/3+1 in {gaussian, expexp, expsoftplus, hill} and rotation (mode-8)%3 in
 // {mobius, hyperbolic, identity}. Reciprocals and exponentials come from the hardware
-// approximations refined to a few ulp (rcp_refined, exp_refined); the identity rotation uses sincosf.
+// approximation refined to a few ulp (rcp_refined) and the hardware exponential (exp_hw); the
+// identity rotation uses sincosf.
 // ---------------------------------------------------------------------------------------------
 enum Radius { CAUCHY = 0, GAUSSIAN = 1, EXPEXP = 2, EXPSOFTPLUS = 3, HILL = 4 };
 enum Rotation { MOBIUS = 0, HYPERBOLIC = 1, IDENTITY = 2 };
@@ -78,6 +79,12 @@ __device__ __forceinline__ float exp_refined(float x) {
     f = fmaf(-k, 1.42860682030941723212e-6f, f);     // ln2 - high part
     return ldexpf(__builtin_amdgcn_exp2f(f * 1.44269504088896341f), (int)k);
 }
+// e^x as the hardware's 2^y of y = x log2(e): relative error about 2^-24 |x| from rounding y plus
+// v_exp_f32's own ulp (|x| <= 36 in the maps: under 3e-6 relative on values below e^-1 wherever
+// |x| > 1, so under 1e-6 absolute); the forward stage maps use it, the backward keeps exp_refined
+__device__ __forceinline__ float exp_hw(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
 
 // r cos(theta) and r sin(theta) of one stage.
 __device__ __forceinline__ void stage_coefficients(float alpha, float beta, int radius_kind,
@@ -93,7 +100,7 @@ __device__ __forceinline__ void stage_coefficients(float alpha, float beta, int 
         s = (small ? (1.0f - square) : (square - 1.0f)) * inv;
     } else if (rotation_kind == HYPERBOLIC) {
         // with e = exp(-|a|): cos = sech(a) = 2e/(1 + e^2), sin = tanh(a) = sign(a) (1 - e^2)/(1 + e^2)
-        const float e = exp_refined(-fabsf(alpha));
+        const float e = exp_hw(-fabsf(alpha));
         const float inv = rcp_refined(fmaf(e, e, 1.0f));
         c = 2.0f * e * inv;
         s = copysignf(fmaf(-e, e, 1.0f) * inv, alpha);
@@ -104,11 +111,11 @@ __device__ __forceinline__ void stage_coefficients(float alpha, float beta, int 
     if (radius_kind == CAUCHY) {
         r = rcp_refined(fmaf(beta, beta, 1.0f));
     } else if (radius_kind == GAUSSIAN) {
-        r = exp_refined(-(beta * beta));
+        r = exp_hw(-(beta * beta));
     } else if (radius_kind == EXPEXP) {
-        r = exp_refined(-exp_refined(fminf(beta, 80.0f)));
+        r = exp_hw(-exp_hw(fminf(beta, 80.0f)));
     } else if (radius_kind == EXPSOFTPLUS) {
-        r = rcp_refined(1.0f + exp_refined(beta));   // exp(-softplus(beta)) = sigmoid(-beta)
+        r = rcp_refined(1.0f + exp_hw(beta));        // exp(-softplus(beta)) = sigmoid(-beta)
     } else {
         const float q = beta * beta;                 // hill: q/(1+q), 1 - 1/(1+q) above q = 1
         const float inv = rcp_refined(1.0f + q);
