@@ -120,6 +120,8 @@ def _case(plugin, torch, batch, tokens, channels, rank, masked=False, with_state
     (3, 4, 32, 16, True, False, "cauchy_x_hyperbolic"),
     (17, 3, 40, 32, False, True, "cauchy_x_identity"),
     (5, 16, 64, 64, True, True, "gaussian_x_mobius"),
+    (9, 19, 48, 48, False, True, "cauchy_x_hyperbolic"),   # unmasked: runs of 6 tokens + 1
+    (6, 32, 40, 32, False, True, "cauchy_x_identity"),    # 5 runs of 6 + 2
 ], ids=lambda a: f"B{a[0]}T{a[1]}C{a[2]}r{a[3]}{'m' if a[4] else ''}{'s' if a[5] else ''}")
 def test_reference_cases(torch_mod, plugin, args):
     _case(plugin, torch_mod, *args)
