@@ -518,9 +518,45 @@ __global__ __launch_bounds__(BLOCK) void lattice_combine(LatticeArgs a) {
     }
 }
 
+// Four consecutive elements as floats, from an address aligned to four elements.
+__device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ float4 load4(const bf16_t *p) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+}
+__device__ __forceinline__ float4 load4(const f16_t *p) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = *reinterpret_cast<const h4 *>(p);
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+// `rows` rows of LEN elements, `stride` elements apart from `src`, into dst[row LEN + e] as
+// floats: four elements a load and one 16-byte LDS store where `vector` says the rows start
+// four-element aligned (the per-element loop cost the replay 16 VALU instructions an element)
+template <typename IO, int LEN>
+__device__ __forceinline__ void stage_rows(float *dst, const IO *src, long long stride, int rows,
+                                           bool vector) {
+    if (LEN % 4 == 0 && vector) {
+        constexpr int Q = LEN / 4;
+        for (int i = threadIdx.x; i < rows * Q; i += BLOCK) {
+            const int r = i / Q, e = 4 * (i % Q);
+            *reinterpret_cast<float4 *>(dst + r * LEN + e) = load4(src + r * stride + e);
+        }
+    } else {
+        for (int i = threadIdx.x; i < rows * LEN; i += BLOCK) {
+            const int r = i / LEN, e = i % LEN;
+            dst[i] = load(src + r * stride + e);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // replay: the scan of one chunk from its entering state, with readout and gate
 // ---------------------------------------------------------------------------------------------
+// K <= 2 runs the scaled token where a channel spans several lanes
+__host__ __device__ constexpr bool replay_scaled(int K, int M) { return K <= 2 && lanes_for(K, M) > 1; }
+
 template <typename IO, int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     constexpr int L = lanes_for(K, M);
@@ -531,7 +567,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     // K <= 2 runs the scaled token (one fused multiply-add per update output) where a channel
     // spans several lanes; a channel on one lane (K d_m <= 32) would hold the unrolled tile's
     // s and nu of every token in registers and keeps the direct form
-    constexpr bool SCALED = K <= 2 && L > 1;
+    constexpr bool SCALED = replay_scaled(K, M);
     static_assert(!SCALED || scaled_coef_count(K) <= NC, "scaled coefficients fit the staged tile");
     const int groups = (a.C + G - 1) / G;
     int block = blockIdx.x;
@@ -544,8 +580,8 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     const int c = group * G + cl;
     const bool active = c < a.C;
 
-    __shared__ float s_write[TT * M];
-    __shared__ float s_read[TT * (K + 1) * M];
+    __shared__ __align__(16) float s_write[TT * M];
+    __shared__ __align__(16) float s_read[TT * (K + 1) * M];
     __shared__ float s_coef[TT * NC * G];
     __shared__ float s_out[TT * G];
     __shared__ unsigned char s_valid[TT];
@@ -572,15 +608,21 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
     const IO *write = static_cast<const IO *>(a.write);
     const IO *read = static_cast<const IO *>(a.read);
     IO *out = static_cast<IO *>(a.out);
+    const auto aligned4 = [](const void *p) {
+        return (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(IO) - 1)) == 0;
+    };
+    // four-element staging in the scaled replay of a compiled-in non-circular map only: the
+    // direct-form kernels measured slower with it (K2 d_m 16 300 -> 421 us, K4 d_m 64 810 -> 907
+    // us) and the circular maps' kernels went past 128 registers (K2 d_m 64 403 -> 498 us)
+    constexpr bool CIRCULAR = MODE == 7 || (MODE >= 8 && (MODE - 8) % 3 == 2);
+    const bool vector_rows = SCALED && MODE != 0 && !CIRCULAR && aligned4(write) &&
+                             aligned4(read) && a.read_row % 4 == 0;
     for (int tile = first; tile < last; tile += TT) {
         const int n = min(TT, last - tile);
         __syncthreads();                                       // previous tile's outputs stored
-        for (int i = threadIdx.x; i < n * M; i += BLOCK)
-            s_write[i] = load(write + ((long long)b * a.T + tile) * M + i);
-        for (int i = threadIdx.x; i < n * (K + 1) * M; i += BLOCK) {
-            const int tt = i / ((K + 1) * M), rest = i % ((K + 1) * M);
-            s_read[i] = load(read + ((long long)b * a.T + tile + tt) * a.read_row + rest);
-        }
+        stage_rows<IO, M>(s_write, write + ((long long)b * a.T + tile) * M, M, n, vector_rows);
+        stage_rows<IO, (K + 1) * M>(s_read, read + ((long long)b * a.T + tile) * a.read_row,
+                                    a.read_row, n, vector_rows);
         stage_coefficient_tile<IO, K, true, MODE, SCALED>(a, b, tile, n, group * G, G, s_coef, s_valid);
         __syncthreads();
         // a full tile of live tokens runs unrolled without branches: the update's outputs then
@@ -632,6 +674,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
                 a.state_out[(((long long)b * K + k) * a.C + c) * M + slot<M, L>(lane, v)] = V[k][v];
     }
 }
+
 
 // ---------------------------------------------------------------------------------------------
 // decode step (T = 1): a stream of the state
