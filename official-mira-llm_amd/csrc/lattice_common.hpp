@@ -29,11 +29,13 @@ __device__ __forceinline__ int slot(int lane, int v) {
     else return v * L + lane;
 }
 
-// DPP lane movement within a 16-lane row.
+// DPP lane movement within a 16-lane row. Every pattern used here reads a lane of the same row,
+// so the bound-zero form changes nothing, and it lets the compiler fold the movement into the
+// consuming add as its DPP operand.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
-                                                              0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xf, 0xf, true));
 }
 
 // Sum over the L lanes of a channel group (adjacent, aligned lanes), in every lane of the group:
