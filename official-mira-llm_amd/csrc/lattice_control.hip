@@ -85,8 +85,7 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
 }
 
 // at least three waves per SIMD: (K, d_m) = (4, 8) would otherwise take 172 VGPRs and two
-// MASKED: the call has a valid mask (the scaled form at K = 2, d_m = 16 serves unmasked calls)
-template <int K, int M, int MODE, bool MASKED>
+template <int K, int M, int MODE>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(3)))
 void lattice_control_kernel(LatticeControlArgs a) {
     using S = Shape<K, M>;
@@ -254,14 +253,6 @@ void lattice_control_kernel(LatticeControlArgs a) {
                           : 0.0f;
     const int mode = MODE ? MODE : a.mode;             // MODE: the stage map compiled in
     const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
-    // K = 2, d_m = 16 without a mask steps in the scaled form (lattice_token_scaled), the stream's
-    // scales here: 64 + 156 VALU a token against 238-250; at d_m 8 and K = 1 the per-token
-    // coefficients cost as much as the slots save, and a mask needs a branch per token (which
-    // makes the compiler copy the update's rotating registers back)
-    constexpr bool SCALED = K == 2 && M == 16 && !MASKED;
-    float sigma[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) sigma[k] = 1.0f;
 
     // tile n: store n - 1, form, scan n, stage n + 1 from `use`, load n + 2 into `fill`
     auto iteration = [&](int n, Pre &fill, const Pre &use) {
@@ -291,29 +282,7 @@ void lattice_control_kernel(LatticeControlArgs a) {
         __syncthreads();
         // ---- scan: every stream forms its own coefficients from the raw columns, then steps;
         // a masked (or absent) row keeps the state and writes 0
-        if constexpr (SCALED) {
-            // every thread steps (no mask), a stream past the batch or the channels on zero
-            // inputs whose output is never stored: a branch here would make the compiler copy the
-            // update's rotating registers back every token
-            static_assert(TT == 1, "one token a tile");
-            const int r = sb;
-            u32x4 raw[COLS / 8];
-#pragma unroll
-            for (int q = 0; q < COLS / 8; ++q)
-                raw[q] = *reinterpret_cast<const u32x4 *>(&s_raw[r][cl * COLS + 8 * q]);
-            auto column = [&](int q) { return bf16_value(raw[q / 8][(q % 8) / 2] >> (16 * (q % 2))); };
-            float rc[K], rs[K], rho[K + 1], staged[scaled_coef_count(K)];
-#pragma unroll
-            for (int k = 0; k < K; ++k)
-                stage_coefficients(column(k), column(K + k), radius_kind, rotation_kind, rc[k], rs[k]);
-#pragma unroll
-            for (int k = 0; k <= K; ++k) rho[k] = column(2 * K + k);
-            stage_scaled_coefficients<K>(staged, 1, rc, rs, bf16_value(s_xg[buf][0][r][cl]), rho,
-                                         silu(bf16_value(s_xg[buf][1][r][cl])));
-            const float y = lattice_token_scaled<K, M, L>(V, sigma, [&](int q) { return staged[q]; },
-                                                          s_write[buf][r], s_read[buf][r], lane);
-            s_out[buf][r][cl] = (uint16_t)bf16_pair(y, 0.0f);
-        } else if (active) {
+        if (active) {
             float mine[TT][NC];
 #pragma unroll
             for (int j = 0; j < TT; ++j) {
@@ -351,29 +320,9 @@ void lattice_control_kernel(LatticeControlArgs a) {
     if (tiles > 1) fetch(p1, 1);
     stage(p0, 0);
     __syncthreads();
-    if constexpr (SCALED) {
-        // six tokens a trip: the update's registers rotate with period three and the prefetch
-        // sets alternate with period two; the scales go back into the state at the trip's end
-        // (and the sequence's), or sooner where one runs small
-        int n = 0;
-        for (; n + 6 <= tiles; n += 6) {
-#pragma unroll
-            for (int j = 0; j < 6; j += 2) {
-                iteration(n + j, p0, p1);
-                iteration(n + j + 1, p1, p0);
-            }
-            scaled_renormalise(V, sigma);
-        }
-        for (; n < tiles; n += 2) {
-            iteration(n, p0, p1);
-            if (n + 1 < tiles) iteration(n + 1, p1, p0);
-        }
-        scaled_renormalise(V, sigma);
-    } else {
-        for (int n = 0; n < tiles; n += 2) {
-            iteration(n, p0, p1);
-            if (n + 1 < tiles) iteration(n + 1, p1, p0);
-        }
+    for (int n = 0; n < tiles; n += 2) {
+        iteration(n, p0, p1);
+        if (n + 1 < tiles) iteration(n + 1, p1, p0);
     }
     store(tiles - 1);
     if (active && a.state_out) {
@@ -385,25 +334,17 @@ void lattice_control_kernel(LatticeControlArgs a) {
     }
 }
 
-template <int K, int M, int MODE, bool MASKED>
-int launch_kmm(const LatticeControlArgs &a, hipStream_t stream) {
+template <int K, int M, int MODE>
+int launch_km(const LatticeControlArgs &a, hipStream_t stream) {
     using S = Shape<K, M>;
     const size_t dynamic = weight_bytes<K, M>(a.R);
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&lattice_control_kernel<K, M, MODE, MASKED>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&lattice_control_kernel<K, M, MODE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)dynamic) != hipSuccess)
         return fail(MIRA_ERR_HIP, "lattice_control_kernel: cannot raise the dynamic LDS limit");
     const long long blocks = (long long)((a.B + S::SB - 1) / S::SB) * ((a.C + S::G - 1) / S::G);
-    hipLaunchKernelGGL((lattice_control_kernel<K, M, MODE, MASKED>), dim3(blocks), dim3(THREADS),
-                       dynamic, stream, a);
+    hipLaunchKernelGGL((lattice_control_kernel<K, M, MODE>), dim3(blocks), dim3(THREADS), dynamic,
+                       stream, a);
     return check_launch("lattice_control_kernel");
-}
-
-template <int K, int M, int MODE>
-int launch_km(const LatticeControlArgs &a, hipStream_t stream) {
-    if constexpr (K == 2 && M == 16) {
-        if (!a.valid) return launch_kmm<K, M, MODE, false>(a, stream);
-    }
-    return launch_kmm<K, M, MODE, true>(a, stream);
 }
 
 // one kernel per stage map

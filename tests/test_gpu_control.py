@@ -73,10 +73,15 @@ def _materialised(plugin, torch, v, order, memory, arch, with_state):
 
 
 def _case(plugin, torch, batch, tokens, channels, rank, masked=False, with_state=False,
-          arch="cauchy_x_mobius", order=2, memory=16, expect_fused=True, oracle=True, seed=0):
+          arch="cauchy_x_mobius", order=2, memory=16, expect_fused=True, oracle=True, seed=0,
+          zero_alpha=False):
     torch.manual_seed(20261011 + batch + tokens + channels + rank)
     v = _inputs(torch, batch, tokens, channels, rank, order, memory, masked, with_state,
                 20261011 + batch + tokens + channels + rank + seed)
+    if zero_alpha:                          # alpha = 0 exactly: the Moebius map's cos is 0
+        lo, hi = v["spans"][0]
+        v["weight"][lo:hi] = 0
+        v["bias"][lo:hi] = 0
     before = plugin.usage()["control"]
     with torch.no_grad():
         got = plugin.matrix_lattice_iir_control(
@@ -125,6 +130,14 @@ def _case(plugin, torch, batch, tokens, channels, rank, masked=False, with_state
 ], ids=lambda a: f"B{a[0]}T{a[1]}C{a[2]}r{a[3]}{'m' if a[4] else ''}{'s' if a[5] else ''}")
 def test_reference_cases(torch_mod, plugin, args):
     _case(plugin, torch_mod, *args)
+
+
+@pytest.mark.parametrize("arch", ["cauchy_x_mobius", "cauchy_x_hyperbolic", "cauchy_x_identity"])
+def test_exact_zero_alpha(torch_mod, plugin, arch):
+    """Every alpha exactly 0 (a zero-initialised projection row): cos = 0 for the Moebius map,
+    sin = 0 for the others, over 30 unmasked tokens with a carried-in state; the output and
+    the final state stay finite and match the oracle."""
+    _case(plugin, torch_mod, 6, 30, 40, 32, False, True, arch, zero_alpha=True)
 
 
 @pytest.mark.parametrize("args", [(192, 257, 1536, 48, False, False, "cauchy_x_mobius"),
