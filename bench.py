@@ -661,7 +661,7 @@ def _cpu_model():
 
 
 def cpu_leg(tokens=8192, channels=2048, runs=3):
-    """The CPU baseline (BASELINE.md section 3): the oracle restatement of the reference CPU
+    """The CPU baseline: the oracle restatement of the reference CPU
     mixer on one cfg2 sequence of `tokens` tokens x `channels` channels, one warm-up and then
     the median of `runs` runs, once on one thread and once on all the host cores this job may
     use (the scan is independent per channel, so each worker process takes an equal channel
@@ -761,8 +761,8 @@ def _cpu_split(kind, jobs, runs):
 
 
 def cpu_gla_leg(tokens=2048, runs=3):
-    """cfg3's CPU baseline on a fixed prefix (SURVEY's rule for the long configs: the cost per
-    token is constant, so the rate extrapolates): all 64 (b, head) streams for `tokens` tokens,
+    """cfg3's CPU baseline on a fixed prefix (the cost per token of the recurrence is constant,
+    so the rate extrapolates to the whole sequence): all 64 (b, head) streams for `tokens` tokens,
     one warm-up, median of `runs`, on one thread and on all the job's cores (4 streams each)."""
     import statistics
 
