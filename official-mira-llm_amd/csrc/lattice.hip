@@ -870,7 +870,19 @@ int launch_typed(LatticeArgs &a, hipStream_t stream) {
     if constexpr (step_kernel_serves(K, M)) {
         const auto aligned16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
         if (a.T == 1 && a.chunks == 1 && aligned16(a.state_in) && aligned16(a.state_out)) {
-            constexpr int CPB = BLOCK / (M / 8);
+            // 1,024-thread blocks where the grid still has >= 2,048 of them (B256 C2048 K2 d_m 64:
+            // 94 -> 88 us); smaller grids lost with them (B64 C2048: 23 -> 25 us), so they keep 256
+            constexpr int WIDE = 1024, CPB_WIDE = WIDE / (M / 8), CPB = BLOCK / (M / 8);
+            const long long wide_blocks = (long long)a.B * ((a.C + CPB_WIDE - 1) / CPB_WIDE);
+            if (wide_blocks >= 2048) {
+                if (a.state_in)
+                    hipLaunchKernelGGL((lattice_step_kernel<IO, K, M, true, WIDE>), dim3(wide_blocks),
+                                       dim3(WIDE), 0, stream, a);
+                else
+                    hipLaunchKernelGGL((lattice_step_kernel<IO, K, M, false, WIDE>), dim3(wide_blocks),
+                                       dim3(WIDE), 0, stream, a);
+                return check_launch("lattice_step_kernel");
+            }
             const long long blocks = (long long)a.B * ((a.C + CPB - 1) / CPB);
             if (a.state_in)
                 hipLaunchKernelGGL((lattice_step_kernel<IO, K, M, true, BLOCK>), dim3(blocks), dim3(BLOCK), 0,

@@ -294,6 +294,24 @@ def test_decode_step_kernel(torch_mod, plugin, order, memory, dtype):
             assert np.array_equal(final[1], initial[1]) and np.array_equal(final[4], initial[4])
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("order,memory", [(2, 64), (1, 128)])
+def test_decode_step_kernel_wide_blocks(torch_mod, plugin, order, memory, dtype):
+    """A batch large enough that the step kernel runs 1,024-thread blocks (>= 2,048 of them):
+    B = 256, a partial channel group (C = 1000), masked sequences, with and without a carried-in
+    state, against the fp64 oracle."""
+    rng = np.random.default_rng(41 + order + memory)
+    B, C = 256, 1000
+    values = L.random_inputs(rng, B, 1, C, order, memory)
+    valid = (rng.random((B, 1)) > 0.1)
+    initial = (rng.standard_normal((B, order, C, memory)) * 0.1).astype(np.float32)
+    for state in (initial, None):
+        y, final = _run(plugin, torch_mod, values, valid, state, dtype=dtype)
+        want_y, want_state = _oracle(values, valid, state, "cauchy_x_hyperbolic", dtype, torch_mod)
+        _assert(y, want_y, dtype, f"wide step output (state {'in' if state is not None else 'none'})")
+        _assert(final, want_state, "float32", "wide step state")
+
+
 def test_reference_geometry_bf16(torch_mod, plugin):
     """The reference mira-s mixer geometry (K=2, d_e=1536, d_m=16) in bf16 at 512 tokens."""
     rng = np.random.default_rng(23)
