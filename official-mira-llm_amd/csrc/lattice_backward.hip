@@ -288,7 +288,14 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
     constexpr int TPO2 = (TPO >= 32) ? 32 : (TPO >= 16) ? 16 : (TPO >= 8) ? 8 : (TPO >= 4) ? 4
                                                             : (TPO >= 2) ? 2 : 1;
     constexpr int PER_PASS = BLOCK / TPO2;
-    static_assert((S * NS + S * NQ * G + 2 * RG * NO) * 4 + S <= 65536, "LDS budget");
+    constexpr int P = S * K * MV > 64 ? 2 : 1;   // passes over the chunk (S is a power of two)
+    constexpr int SP = S / P;
+    // the channel sums are double-buffered by token parity (one barrier a token) unless a single
+    // buffer and a second barrier let more blocks share a CU's 160 KiB of LDS
+    constexpr int LDS_ONE = (S * NS + S * NQ * G + RG * NO) * 4 + S;
+    constexpr int LDS_TWO = LDS_ONE + RG * NO * 4;
+    constexpr int RED_BUFFERS = 163840 / LDS_ONE > 163840 / LDS_TWO ? 1 : 2;
+    static_assert(LDS_ONE + (RED_BUFFERS - 1) * RG * NO * 4 <= 65536, "LDS budget");
     int block = blockIdx.x;
     const int group = block % a.groups;
     block /= a.groups;
@@ -300,7 +307,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
 
     __shared__ float s_sn[S * NS];
     __shared__ float s_tc[S * NQ * G];
-    __shared__ __align__(16) float s_red[2][RG * NO];   // double-buffered: one barrier a token
+    __shared__ __align__(16) float s_red[RED_BUFFERS][RG * NO];
     __shared__ unsigned char s_valid[S];
     const IO *write = static_cast<const IO *>(a.write);
     const IO *read = static_cast<const IO *>(a.read);
@@ -333,136 +340,156 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
         }
     __syncthreads();
 
-    // forward: the state entering every token of the chunk
-    float Vs[S][K][MV];
+    // The chunk goes backward in P passes of SP tokens, last pass first; each pass recomputes the
+    // forward from the chunk's entering state and keeps the states entering its own SP tokens.
+    // Two passes halve the registers of the kept states (S K MV = 128 floats at 16 tokens) for 8
+    // more forward tokens a chunk.
+    float V0[K][MV];
 #pragma unroll
-    for (int t = 0; t < S; ++t) {
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int v = 0; v < MV; ++v) V0[k][v] = V[k][v];
+#pragma unroll
+    for (int pass = P - 1; pass >= 0; --pass) {
+        if (pass * SP >= n) continue;                                  // uniform over the block
 #pragma unroll
         for (int k = 0; k < K; ++k)
 #pragma unroll
-            for (int v = 0; v < MV; ++v) Vs[t][k][v] = V[k][v];
-        if (t < n && s_valid[t]) {
-            const float *q = s_tc + t * NQ * G + cl;
-            float rc[K], rs[K];
+            for (int v = 0; v < MV; ++v) V[k][v] = V0[k][v];
+        // forward: the state entering every token of the pass
+        float Vs[SP][K][MV];
 #pragma unroll
-            for (int k = 0; k < K; ++k) { rc[k] = q[k * G]; rs[k] = q[(K + k) * G]; }
-            const float xv = q[(3 * K + 1) * G];
+        for (int t = 0; t < (pass + 1) * SP; ++t) {
+            if (t >= pass * SP) {
 #pragma unroll
-            for (int v = 0; v < MV; ++v) {
-                float U = xv * s_sn[t * NS + slot<M, L>(lane, v)];
+                for (int k = 0; k < K; ++k)
 #pragma unroll
-                for (int k = K; k >= 1; --k) {
-                    const float delayed = V[k - 1][v];
-                    const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
-                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
-                    if (k < K) V[k][v] = level;
+                    for (int v = 0; v < MV; ++v) Vs[t - pass * SP][k][v] = V[k][v];
+            }
+            if (t < n && s_valid[t] && t + 1 < (pass + 1) * SP) {
+                const float *q = s_tc + t * NQ * G + cl;
+                float rc[K], rs[K];
+#pragma unroll
+                for (int k = 0; k < K; ++k) { rc[k] = q[k * G]; rs[k] = q[(K + k) * G]; }
+                const float xv = q[(3 * K + 1) * G];
+#pragma unroll
+                for (int v = 0; v < MV; ++v) {
+                    float U = xv * s_sn[t * NS + slot<M, L>(lane, v)];
+#pragma unroll
+                    for (int k = K; k >= 1; --k) {
+                        const float delayed = V[k - 1][v];
+                        const float level = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                        U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                        if (k < K) V[k][v] = level;
+                    }
+                    V[0][v] = U;
                 }
-                V[0][v] = U;
             }
         }
-    }
 
-    // backward, token by token
+        // backward, token by token
 #pragma unroll
-    for (int t = S - 1; t >= 0; --t) {
-        if (t >= n) continue;                                   // uniform over the block
-        float sums[NQ];
-        float red[K + 2][MV];
+        for (int t = (pass + 1) * SP - 1; t >= pass * SP; --t) {
+            if (t >= n) continue;                                   // uniform over the block
+            float sums[NQ];
+            float red[K + 2][MV];
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) sums[q] = 0.0f;
+            for (int q = 0; q < NQ; ++q) sums[q] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < K + 2; ++kk)
+            for (int kk = 0; kk < K + 2; ++kk)
 #pragma unroll
-            for (int v = 0; v < MV; ++v) red[kk][v] = 0.0f;
-        if (s_valid[t]) {
-            const float *q = s_tc + t * NQ * G + cl;
-            float rc[K], rs[K], er[K + 1];
+                for (int v = 0; v < MV; ++v) red[kk][v] = 0.0f;
+            if (s_valid[t]) {
+                const float *q = s_tc + t * NQ * G + cl;
+                float rc[K], rs[K], er[K + 1];
 #pragma unroll
-            for (int k = 0; k < K; ++k) { rc[k] = q[k * G]; rs[k] = q[(K + k) * G]; }
+                for (int k = 0; k < K; ++k) { rc[k] = q[k * G]; rs[k] = q[(K + k) * G]; }
 #pragma unroll
-            for (int k = 0; k <= K; ++k) er[k] = q[(2 * K + k) * G];
-            const float xv = q[(3 * K + 1) * G];
-            const float *sw = s_sn + t * NS;
-            const float *nu = sw + M;
+                for (int k = 0; k <= K; ++k) er[k] = q[(2 * K + k) * G];
+                const float xv = q[(3 * K + 1) * G];
+                const float *sw = s_sn + t * NS;
+                const float *nu = sw + M;
 #pragma unroll
-            for (int v = 0; v < MV; ++v) {
-                const int m = slot<M, L>(lane, v);
-                const float sm = sw[m];
-                float Uin[K + 1], level[K + 1];
-                float U = xv * sm;
+                for (int v = 0; v < MV; ++v) {
+                    const int m = slot<M, L>(lane, v);
+                    const float sm = sw[m];
+                    float Uin[K + 1], level[K + 1];
+                    float U = xv * sm;
 #pragma unroll
-                for (int k = K; k >= 1; --k) {
-                    const float delayed = Vs[t][k - 1][v];
-                    Uin[k] = U;
-                    level[k] = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
-                    U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
-                }
-                level[0] = U;
-                float Lam[K + 1];
+                    for (int k = K; k >= 1; --k) {
+                        const float delayed = Vs[t - pass * SP][k - 1][v];
+                        Uin[k] = U;
+                        level[k] = fmaf(rc[k - 1], delayed, rs[k - 1] * U);
+                        U = fmaf(rc[k - 1], U, -(rs[k - 1] * delayed));
+                    }
+                    level[0] = U;
+                    float Lam[K + 1];
 #pragma unroll
-                for (int k = 0; k <= K; ++k) {
-                    const float nk = nu[k * M + m];
-                    sums[2 * K + k] = fmaf(level[k], nk, sums[2 * K + k]);            // P_k
-                    Lam[k] = fmaf(er[k], nk, k < K ? lam[k][v] : 0.0f);
-                    red[1 + k][v] = er[k] * level[k];                               // dnu_k
-                }
-                float dU = Lam[0];
+                    for (int k = 0; k <= K; ++k) {
+                        const float nk = nu[k * M + m];
+                        sums[2 * K + k] = fmaf(level[k], nk, sums[2 * K + k]);            // P_k
+                        Lam[k] = fmaf(er[k], nk, k < K ? lam[k][v] : 0.0f);
+                        red[1 + k][v] = er[k] * level[k];                               // dnu_k
+                    }
+                    float dU = Lam[0];
 #pragma unroll
-                for (int k = 1; k <= K; ++k) {
-                    const float delayed = Vs[t][k - 1][v];
-                    sums[K + k - 1] = fmaf(Lam[k], Uin[k], fmaf(-dU, delayed, sums[K + k - 1]));
-                    sums[k - 1] = fmaf(Lam[k], delayed, fmaf(dU, Uin[k], sums[k - 1]));
-                    const float next = fmaf(rc[k - 1], Lam[k], -(rs[k - 1] * dU));
-                    dU = fmaf(rs[k - 1], Lam[k], rc[k - 1] * dU);
-                    lam[k - 1][v] = next;
-                }
-                sums[3 * K + 1] = fmaf(dU, sm, sums[3 * K + 1]);                     // dx
-                red[0][v] = dU * xv;                                                 // ds
-            }
-        }
-        // per (token, channel): the sums over the channel's lanes replace the staged quantities
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) sums[q] = lane_sum<L>(sums[q]);
-        if (active && lane == 0) {
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) s_tc[(t * NQ + q) * G + cl] = sums[q];
-        }
-        // per (token, slot): the channel group's sums -- a row's channels added with DPP, then
-        // one set per row (or per wide channel) through LDS, double-buffered by token parity
-        float *red_buffer = s_red[t & 1];
-        const int rowgroup = L < 16 ? (int)threadIdx.x / 16 : cl;
-        const bool writer = L < 16 ? ((int)threadIdx.x % 16) < L : true;
-#pragma unroll
-        for (int kk = 0; kk < K + 2; ++kk) {
-#pragma unroll
-            for (int v = 0; v < MV; ++v) {
-                float value = active ? red[kk][v] : 0.0f;
-                if constexpr (L < 16) value = row_channel_sum<L>(value);
-                red[kk][v] = value;
-            }
-            if (writer) {
-                float *dst = red_buffer + rowgroup * NO + kk * M;
-                if constexpr (MV % 4 == 0) {
-#pragma unroll
-                    for (int v = 0; v < MV; v += 4)
-                        *reinterpret_cast<float4 *>(dst + slot<M, L>(lane, v)) =
-                            make_float4(red[kk][v], red[kk][v + 1], red[kk][v + 2], red[kk][v + 3]);
-                } else {
-#pragma unroll
-                    for (int v = 0; v < MV; ++v) dst[slot<M, L>(lane, v)] = red[kk][v];
+                    for (int k = 1; k <= K; ++k) {
+                        const float delayed = Vs[t - pass * SP][k - 1][v];
+                        sums[K + k - 1] = fmaf(Lam[k], Uin[k], fmaf(-dU, delayed, sums[K + k - 1]));
+                        sums[k - 1] = fmaf(Lam[k], delayed, fmaf(dU, Uin[k], sums[k - 1]));
+                        const float next = fmaf(rc[k - 1], Lam[k], -(rs[k - 1] * dU));
+                        dU = fmaf(rs[k - 1], Lam[k], rc[k - 1] * dU);
+                        lam[k - 1][v] = next;
+                    }
+                    sums[3 * K + 1] = fmaf(dU, sm, sums[3 * K + 1]);                     // dx
+                    red[0][v] = dU * xv;                                                 // ds
                 }
             }
-        }
-        __syncthreads();
-        const long long out_row = ((long long)group * a.B + b) * a.T + first + t;
+            // per (token, channel): the sums over the channel's lanes replace the staged quantities
 #pragma unroll
-        for (int o0 = 0; o0 < NO; o0 += PER_PASS) {
-            const int o = o0 + threadIdx.x / TPO2, part = threadIdx.x % TPO2;
-            float total = 0.0f;
-            if (o < NO)
-                for (int g = part; g < RG; g += TPO2) total += red_buffer[g * NO + o];
-            total = group_sum<TPO2>(total);
-            if (o < NO && part == 0) a.partial[out_row * NO + o] = total;
+            for (int q = 0; q < NQ; ++q) sums[q] = lane_sum<L>(sums[q]);
+            if (active && lane == 0) {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) s_tc[(t * NQ + q) * G + cl] = sums[q];
+            }
+            // per (token, slot): the channel group's sums -- a row's channels added with DPP, then
+            // one set per row (or per wide channel) through LDS, double-buffered by token parity
+            float *red_buffer = s_red[t % RED_BUFFERS];
+            const int rowgroup = L < 16 ? (int)threadIdx.x / 16 : cl;
+            const bool writer = L < 16 ? ((int)threadIdx.x % 16) < L : true;
+#pragma unroll
+            for (int kk = 0; kk < K + 2; ++kk) {
+#pragma unroll
+                for (int v = 0; v < MV; ++v) {
+                    float value = active ? red[kk][v] : 0.0f;
+                    if constexpr (L < 16) value = row_channel_sum<L>(value);
+                    red[kk][v] = value;
+                }
+                if (writer) {
+                    float *dst = red_buffer + rowgroup * NO + kk * M;
+                    if constexpr (MV % 4 == 0) {
+#pragma unroll
+                        for (int v = 0; v < MV; v += 4)
+                            *reinterpret_cast<float4 *>(dst + slot<M, L>(lane, v)) =
+                                make_float4(red[kk][v], red[kk][v + 1], red[kk][v + 2], red[kk][v + 3]);
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < MV; ++v) dst[slot<M, L>(lane, v)] = red[kk][v];
+                    }
+                }
+            }
+            __syncthreads();
+            const long long out_row = ((long long)group * a.B + b) * a.T + first + t;
+#pragma unroll
+            for (int o0 = 0; o0 < NO; o0 += PER_PASS) {
+                const int o = o0 + threadIdx.x / TPO2, part = threadIdx.x % TPO2;
+                float total = 0.0f;
+                if (o < NO)
+                    for (int g = part; g < RG; g += TPO2) total += red_buffer[g * NO + o];
+                total = group_sum<TPO2>(total);
+                if (o < NO && part == 0) a.partial[out_row * NO + o] = total;
+            }
+            if constexpr (RED_BUFFERS == 1) __syncthreads();   // the next token's sums reuse the buffer
         }
     }
 
