@@ -106,7 +106,7 @@ int mira_lattice_forward_static(const void *x, int64_t x_row, const void *alpha,
  * Every gradient is written in x's dtype at its own row stride (so the caller may point them at
  * views of packed projection gradients); with raw_write non-NULL ([B,T,M] at raw_write_row),
  * grad_write receives the gradient of the raw write, d/dz of SiLU(z) applied. workspace: at least
- * mira_lattice_backward_workspace_bytes(B,T,C,K,M) bytes. */
+ * mira_lattice_backward_workspace_bytes(B,T,C,K,M) bytes, 16-byte aligned. */
 int mira_lattice_backward_chunk(int K, int M);
 size_t mira_lattice_backward_workspace_bytes(int B, int T, int C, int K, int M);
 int mira_lattice_backward(const void *x, int64_t x_row, const void *alpha, int64_t alpha_row,

@@ -230,6 +230,8 @@ int mira_lattice_backward(const void *x, int64_t x_row, const void *alpha, int64
     const size_t need = lattice_backward_workspace(B, T, C, K, M);
     if (!workspace || workspace_bytes < need)
         return fail(MIRA_ERR_ARG, "mira: workspace smaller than mira_lattice_backward_workspace_bytes");
+    if (reinterpret_cast<uintptr_t>(workspace) % 16)
+        return fail(MIRA_ERR_ARG, "mira: the backward workspace must be 16-byte aligned");
     float *base = static_cast<float *>(workspace);
     a.adjoint = a.chunks > 1 ? base : nullptr;
     a.partial = base + (a.chunks > 1 ? (long long)B * a.chunks * C * K * M : 0);

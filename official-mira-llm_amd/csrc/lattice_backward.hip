@@ -544,22 +544,44 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
 // ---------------------------------------------------------------------------------------------
 template <typename IO>
 __global__ __launch_bounds__(BLOCK) void lattice_backward_reduce(LatticeBackArgs a) {
+    // a thread takes four consecutive sums (one 16-byte load a group; (K + 2) d_m is a multiple
+    // of four, so the four share a token and a quantity) and keeps eight groups' loads in flight;
+    // each sum still adds the groups in order from zero
+    constexpr int AHEAD = 8;
     const int NO = (a.K + 2) * a.M;
-    const long long index = (long long)blockIdx.x * BLOCK + threadIdx.x;
+    const long long index = ((long long)blockIdx.x * BLOCK + threadIdx.x) * 4;
     const long long per_group = (long long)a.B * a.T * NO;
     if (index >= per_group) return;
-    float total = 0.0f;
-    for (int g = 0; g < a.groups; ++g) total += a.partial[g * per_group + index];
+    const float4 *part = reinterpret_cast<const float4 *>(a.partial + index);
+    const long long stride = per_group / 4;
+    float total[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int g = 0;
+    for (; g + AHEAD <= a.groups; g += AHEAD) {
+        float4 v[AHEAD];
+#pragma unroll
+        for (int u = 0; u < AHEAD; ++u) v[u] = part[(g + u) * stride];
+#pragma unroll
+        for (int u = 0; u < AHEAD; ++u) {
+            total[0] += v[u].x; total[1] += v[u].y; total[2] += v[u].z; total[3] += v[u].w;
+        }
+    }
+    for (; g < a.groups; ++g) {
+        const float4 v = part[g * stride];
+        total[0] += v.x; total[1] += v.y; total[2] += v.z; total[3] += v.w;
+    }
     const long long row = index / NO;
     const int o = index % NO;
     const int kk = o / a.M, m = o % a.M;
-    if (kk == 0) {
-        if (a.raw_write)
-            total *= silu_slope(load(static_cast<const IO *>(a.raw_write) + row * a.raw_write_row + m));
-        static_cast<IO *>(a.grad_write)[row * a.grad_write_row + m] = from_float<IO>(total);
-    } else {
-        static_cast<IO *>(a.grad_read)[row * a.grad_read_row + (kk - 1) * a.M + m] =
-            from_float<IO>(total);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (kk == 0) {
+            if (a.raw_write)
+                total[e] *= silu_slope(load(static_cast<const IO *>(a.raw_write) + row * a.raw_write_row + m + e));
+            static_cast<IO *>(a.grad_write)[row * a.grad_write_row + m + e] = from_float<IO>(total[e]);
+        } else {
+            static_cast<IO *>(a.grad_read)[row * a.grad_read_row + (kk - 1) * a.M + m + e] =
+                from_float<IO>(total[e]);
+        }
     }
 }
 
@@ -583,8 +605,9 @@ int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
     const long long blocks = (long long)a.B * a.chunks * a.groups;
     hipLaunchKernelGGL((lattice_backward_replay<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
     if (int rc = check_launch("lattice_backward_replay")) return rc;
-    const long long values = (long long)a.B * a.T * (K + 2) * M;
-    hipLaunchKernelGGL((lattice_backward_reduce<IO>), dim3((values + BLOCK - 1) / BLOCK),
+    static_assert((K + 2) * M % 4 == 0, "the reduce takes four sums a thread");
+    const long long threads = (long long)a.B * a.T * (K + 2) * M / 4;
+    hipLaunchKernelGGL((lattice_backward_reduce<IO>), dim3((threads + BLOCK - 1) / BLOCK),
                        dim3(BLOCK), 0, stream, a);
     return check_launch("lattice_backward_reduce");
 }
