@@ -836,12 +836,14 @@ def main():
         legs.discard("stack")
     prefill = prefill_leg(torch, mira, args.steps, args.warmup)
     decode = decode_leg(torch, mira, args.decode_steps) if "decode" in legs else None
-    gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 3) if "gla" in legs else None
-    lat = lattice_leg(torch, mira, max(5, args.steps // 5), 2) if "lattice" in legs else None
-    ctl = control_leg(torch, mira, max(5, args.steps // 10), 3) if "control" in legs else None
-    back = backward_leg(torch, mira, max(3, args.steps // 10), 2) if "backward" in legs else None
-    mix = mixer_leg(torch, mira, 3, 1) if "mixer" in legs else None
-    stack = stack_leg(torch, 3, 1) if "stack" in legs else None
+    # every leg warms up for at least ~5 ms of its own calls first: with two warm-up calls the
+    # lattice operator's first timed calls still ran ~20 % slower than its steady state
+    gla = gla_prefill_leg(torch, mira, max(5, args.steps // 2), 10) if "gla" in legs else None
+    lat = lattice_leg(torch, mira, max(10, args.steps // 2), 10) if "lattice" in legs else None
+    ctl = control_leg(torch, mira, max(5, args.steps // 10), 5) if "control" in legs else None
+    back = backward_leg(torch, mira, max(3, args.steps // 10), 3) if "backward" in legs else None
+    mix = mixer_leg(torch, mira, 3, 3) if "mixer" in legs else None
+    stack = stack_leg(torch, 3, 2) if "stack" in legs else None
     achieved = prefill["algorithmic"] / prefill["kernel_s"] / 1e9
     line = {
         "metric": METRIC,
