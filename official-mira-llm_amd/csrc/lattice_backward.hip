@@ -53,6 +53,19 @@ __host__ __device__ constexpr int back_chunk_for(int K, int M) {
     return S;
 }
 
+// lanes per channel in the adjoint summary: it keeps only the adjoint and sums nothing over lanes,
+// so a lane may hold up to 16 floats of it, and a block takes up to 64 channels while their staged
+// per-(token, channel) quantities fit 32 KiB: the block's read vectors, staged once, then serve
+// more channels (32 floats a lane at K2 d_m 64 took 129 VGPRs, three waves a SIMD, and lost)
+__host__ __device__ constexpr int summary_lanes(int K, int M) {
+    const int S = back_chunk_for(K, M);
+    int L = back_lanes(K, M);
+    while (L > 1 && K * M / (L / 2) <= 16 && BLOCK / (L / 2) <= 64 &&
+           S * (3 * K + 1) * (BLOCK / (L / 2)) * 4 <= 32768)
+        L /= 2;
+    return L;
+}
+
 // the (K, d_m) with backward kernels: the reference plugin's ORDER_MEMORIES
 // (kernel/cuda/mira_dspv2/mira.py:185-190)
 __host__ __device__ constexpr bool backward_serves(int K, int M) {
@@ -154,13 +167,14 @@ __device__ __forceinline__ void stage_adjoint_tile(const LatticeBackArgs &a, int
 // ---------------------------------------------------------------------------------------------
 template <typename IO, int K, int M>
 __global__ __launch_bounds__(BLOCK) void lattice_adjoint_summary(LatticeBackArgs a) {
-    constexpr int L = back_lanes(K, M), G = BLOCK / L, MV = M / L;
+    constexpr int L = summary_lanes(K, M), G = BLOCK / L, MV = M / L;
     constexpr int S = back_chunk_for(K, M);
     constexpr int NQ = 3 * K + 1;
     constexpr int NR = (K + 1) * M;
+    const int groups = (a.C + G - 1) / G;
     int block = blockIdx.x;
-    const int group = block % a.groups;
-    block /= a.groups;
+    const int group = block % groups;
+    block /= groups;
     const int j = 1 + block % (a.chunks - 1);
     const int b = block / (a.chunks - 1);
     const int lane = threadIdx.x % L, cl = threadIdx.x / L, c = group * G + cl;
@@ -593,7 +607,8 @@ int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
                                   "mira_lattice_backward_chunk's chunk length");
     a.groups = (a.C + G - 1) / G;
     if (a.chunks > 1) {
-        const long long blocks = (long long)a.B * (a.chunks - 1) * a.groups;
+        constexpr int GS = BLOCK / summary_lanes(K, M);
+        const long long blocks = (long long)a.B * (a.chunks - 1) * ((a.C + GS - 1) / GS);
         hipLaunchKernelGGL((lattice_adjoint_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0,
                            stream, a);
         if (int rc = check_launch("lattice_adjoint_summary")) return rc;
