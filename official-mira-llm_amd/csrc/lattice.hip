@@ -593,8 +593,11 @@ __global__ __launch_bounds__(BLOCK) void lattice_replay(LatticeArgs a) {
             float value = 0.0f;
             if (active) {
                 const int m = slot<M, L>(lane, v);
-                if (chunk_index > 0)
-                    value = a.carry[((((long long)b * a.chunks + chunk_index) * a.C + c) * K + k) * M + m];
+                if (chunk_index > 0) {
+                    const long long plane = (long long)b * (a.carry_chunks ? a.carry_chunks : a.chunks) +
+                                            (long long)chunk_index * (a.carry_step ? a.carry_step : 1);
+                    value = a.carry[((plane * a.C + c) * K + k) * M + m];
+                }
                 else if (a.state_in)
                     value = a.state_in[(((long long)b * K + k) * a.C + c) * M + m];
             }
@@ -853,8 +856,20 @@ int launch_chunked(LatticeArgs &a, hipStream_t stream) {
                            0, stream, a);
         if (int rc = check_launch("lattice_combine")) return rc;
     }
-    const long long blocks = (long long)a.B * a.chunks * groups;
-    hipLaunchKernelGGL((lattice_replay<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+    // A call cut finer than the plan (a training forward runs at the backward's 16-token chunks,
+    // whose entering states the backward reads) replays at the planned length, entering each
+    // replay chunk from every step-th chunk's state: the carries it reads shrink by that step
+    // and each block scans more tokens.
+    LatticeArgs r = a;
+    const int plan = lattice_plan_chunk(a.B, a.T, a.C, K, M);
+    if (a.chunks > 1 && plan > a.chunk && plan % a.chunk == 0) {
+        r.chunk = plan;
+        r.chunks = (a.T + plan - 1) / plan;
+        r.carry_chunks = a.chunks;
+        r.carry_step = plan / a.chunk;
+    }
+    const long long blocks = (long long)r.B * r.chunks * groups;
+    hipLaunchKernelGGL((lattice_replay<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0, stream, r);
     return check_launch("lattice_replay");
 }
 

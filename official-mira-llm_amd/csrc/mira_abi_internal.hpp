@@ -33,6 +33,8 @@ struct LatticeArgs {
     int chunk, chunks;
     float *phi;                                // [B,chunks,C,K,K]
     float *carry;                              // [B,chunks,C,K,M]
+    int carry_chunks, carry_step;              // the replay's view of the carries: planes per
+                                               // sequence and per replay chunk (0: chunks, 1)
 };
 bool lattice_supported(int K, int M, int dtype);
 int lattice_lanes(int K, int M);
