@@ -14,7 +14,8 @@
 //   combine  per (b, c, m): S_(j+1) = Phi_j S_j + carry_j over the chunks, writing the state that
 //            enters every chunk over its carry slot.
 //   replay   per (b, chunk, c): the chunk from its entering state with the readout and the gate;
-//            the last chunk stores the final state. With one chunk this is the whole scan, and at
+//            the last chunk stores the final state. A call cut finer than the planned chunk
+//            length replays at the planned length from every step-th entering state. With one chunk this is the whole scan, and at
 //            T = 1 it is the decode step. Stage K's level is never kept, so the replay reads it
 //            out as rc_K sum_m V^(K-1) nu_K + rs_K x sum_m s nu_K instead of forming it per m:
 //            5K - 1 operations per (t, c, m) instead of 5K + 2. At K <= 2, with a channel on
