@@ -23,14 +23,17 @@
 //   reduce            ds and dnu sum over channels: each replay block leaves its channel group's
 //                     sums per (b, t), and one pass adds the groups (and applies SiLU' when the
 //                     caller wants the gradient of the raw write).
-// The chunk is short (<= 16 tokens) so that a lane keeps the state entering every token of its
-// chunk in registers (<= 128 floats). Per-(token, channel) sums over a channel's lanes use DPP;
-// per-(token, slot) sums over the channels of a block are first added across a 16-lane row's
-// channels with DPP, then go through a double-buffered LDS tile (one barrier a token).
+// The chunk is short (<= 16 tokens) so that a lane keeps the states entering the tokens of its
+// chunk in registers: all of them (<= 64 floats), or half of them in each of two passes over the
+// chunk. Per-(token, channel) sums over a channel's lanes use DPP; per-(token, slot) sums over
+// the channels of a block are first added across a 16-lane row's channels with DPP, then go
+// through an LDS tile, double-buffered (one barrier a token) unless a single buffer (two
+// barriers) lets another block share the CU.
 #include "lattice_common.hpp"
 #include "mira_abi_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mira {
 namespace {
@@ -130,13 +133,15 @@ __device__ __forceinline__ float silu_slope(float g) {
 }
 
 // Stage a chunk's per-(token, channel) quantities, [token][quantity][channel]:
-// rc[K], rs[K], e rho[K+1] (e = dy SiLU(gamma)) and, with X, x.
-template <typename IO, int K, bool X>
+// rc[K], rs[K], e rho[K+1] (e = dy SiLU(gamma)) and, with X, x. MODE is the stage mode when the
+// kernel is built for one stage map, 0 when it reads a.mode.
+template <typename IO, int K, bool X, int MODE>
 __device__ __forceinline__ void stage_adjoint_tile(const LatticeBackArgs &a, int b, int first,
                                                    int n, int c0, int G, float *tc,
                                                    unsigned char *valid) {
     constexpr int NQ = 3 * K + 1 + (X ? 1 : 0);
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    const int mode = MODE ? MODE : a.mode;
+    const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
     for (int i = threadIdx.x; i < n * G; i += BLOCK) {
         const int tt = i / G, cl = i % G, c = c0 + cl;
         if (c >= a.C) continue;
@@ -165,7 +170,7 @@ __device__ __forceinline__ void stage_adjoint_tile(const LatticeBackArgs &a, int
 // ---------------------------------------------------------------------------------------------
 // adjoint summary: lambda at the start of chunk j > 0 from a zero adjoint at its end
 // ---------------------------------------------------------------------------------------------
-template <typename IO, int K, int M>
+template <typename IO, int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_adjoint_summary(LatticeBackArgs a) {
     constexpr int L = summary_lanes(K, M), G = BLOCK / L, MV = M / L;
     constexpr int S = back_chunk_for(K, M);
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_adjoint_summary(LatticeBackArgs
         const int tt = i / NR, rest = i % NR;
         s_nu[i] = load(read + ((long long)b * a.T + first + tt) * a.read_row + rest);
     }
-    stage_adjoint_tile<IO, K, false>(a, b, first, n, group * G, G, s_tc, s_valid);
+    stage_adjoint_tile<IO, K, false, MODE>(a, b, first, n, group * G, G, s_tc, s_valid);
     __syncthreads();
     if (c >= a.C) return;
     float lam[K][MV];
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_adjoint_combine(LatticeBackArgs
 // ---------------------------------------------------------------------------------------------
 // backward replay: one chunk of one channel group, every gradient
 // ---------------------------------------------------------------------------------------------
-template <typename IO, int K, int M>
+template <typename IO, int K, int M, int MODE>
 __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs a) {
     constexpr int L = back_lanes(K, M), G = BLOCK / L, MV = M / L;
     constexpr int S = back_chunk_for(K, M);
@@ -330,7 +335,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
         const long long row = (long long)b * a.T + first + tt;
         s_sn[i] = rest < M ? load(write + row * M + rest) : load(read + row * a.read_row + (rest - M));
     }
-    stage_adjoint_tile<IO, K, true>(a, b, first, n, group * G, G, s_tc, s_valid);
+    stage_adjoint_tile<IO, K, true, MODE>(a, b, first, n, group * G, G, s_tc, s_valid);
 
     // the state entering the chunk and the adjoint at its end
     float V[K][MV], lam[K][MV];
@@ -508,7 +513,8 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_replay(LatticeBackArgs
     }
 
     // per (token, channel) gradients, one thread per pair
-    const int radius_kind = radius_of(a.mode), rotation_kind = rotation_of(a.mode);
+    const int mode = MODE ? MODE : a.mode;
+    const int radius_kind = radius_of(mode), rotation_kind = rotation_of(mode);
     for (int i = threadIdx.x; i < n * G; i += BLOCK) {
         const int tt = i / G, q = i % G, ch = group * G + q;
         if (ch >= a.C) continue;
@@ -599,7 +605,7 @@ __global__ __launch_bounds__(BLOCK) void lattice_backward_reduce(LatticeBackArgs
     }
 }
 
-template <typename IO, int K, int M>
+template <typename IO, int K, int M, int MODE>
 int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
     constexpr int G = BLOCK / back_lanes(K, M);
     if (a.chunk != back_chunk_for(K, M))
@@ -609,7 +615,7 @@ int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
     if (a.chunks > 1) {
         constexpr int GS = BLOCK / summary_lanes(K, M);
         const long long blocks = (long long)a.B * (a.chunks - 1) * ((a.C + GS - 1) / GS);
-        hipLaunchKernelGGL((lattice_adjoint_summary<IO, K, M>), dim3(blocks), dim3(BLOCK), 0,
+        hipLaunchKernelGGL((lattice_adjoint_summary<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0,
                            stream, a);
         if (int rc = check_launch("lattice_adjoint_summary")) return rc;
         const long long threads = (long long)a.B * a.C * M;
@@ -618,7 +624,7 @@ int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
         if (int rc = check_launch("lattice_adjoint_combine")) return rc;
     }
     const long long blocks = (long long)a.B * a.chunks * a.groups;
-    hipLaunchKernelGGL((lattice_backward_replay<IO, K, M>), dim3(blocks), dim3(BLOCK), 0, stream, a);
+    hipLaunchKernelGGL((lattice_backward_replay<IO, K, M, MODE>), dim3(blocks), dim3(BLOCK), 0, stream, a);
     if (int rc = check_launch("lattice_backward_replay")) return rc;
     static_assert((K + 2) * M % 4 == 0, "the reduce takes four sums a thread");
     const long long threads = (long long)a.B * a.T * (K + 2) * M / 4;
@@ -627,13 +633,39 @@ int launch_backward(LatticeBackArgs &a, hipStream_t stream) {
     return check_launch("lattice_backward_reduce");
 }
 
+// bf16 at the mixer's two geometries (K 2 with d_m 16 and 64) runs backward kernels built for
+// their one stage map, as the forward does; everything else reads the map at run time
+template <typename IO, int K, int M>
+int backward_map(LatticeBackArgs &a, hipStream_t s) {
+    if constexpr (std::is_same<IO, bf16_t>::value && K == 2 && (M == 16 || M == 64)) {
+        switch (a.mode) {
+            case 3: return launch_backward<IO, K, M, 3>(a, s);
+            case 6: return launch_backward<IO, K, M, 6>(a, s);
+            case 7: return launch_backward<IO, K, M, 7>(a, s);
+            case 8: return launch_backward<IO, K, M, 8>(a, s);
+            case 9: return launch_backward<IO, K, M, 9>(a, s);
+            case 10: return launch_backward<IO, K, M, 10>(a, s);
+            case 11: return launch_backward<IO, K, M, 11>(a, s);
+            case 12: return launch_backward<IO, K, M, 12>(a, s);
+            case 13: return launch_backward<IO, K, M, 13>(a, s);
+            case 14: return launch_backward<IO, K, M, 14>(a, s);
+            case 15: return launch_backward<IO, K, M, 15>(a, s);
+            case 16: return launch_backward<IO, K, M, 16>(a, s);
+            case 17: return launch_backward<IO, K, M, 17>(a, s);
+            case 18: return launch_backward<IO, K, M, 18>(a, s);
+            case 19: return launch_backward<IO, K, M, 19>(a, s);
+        }
+    }
+    return launch_backward<IO, K, M, 0>(a, s);
+}
+
 template <typename IO, int K>
 int backward_m(LatticeBackArgs &a, hipStream_t s) {
     switch (a.M) {
-        case 8: return launch_backward<IO, K, 8>(a, s);
-        case 16: return launch_backward<IO, K, 16>(a, s);
-        case 32: if constexpr (backward_serves(K, 32)) return launch_backward<IO, K, 32>(a, s); break;
-        case 64: if constexpr (backward_serves(K, 64)) return launch_backward<IO, K, 64>(a, s); break;
+        case 8: return backward_map<IO, K, 8>(a, s);
+        case 16: return backward_map<IO, K, 16>(a, s);
+        case 32: if constexpr (backward_serves(K, 32)) return backward_map<IO, K, 32>(a, s); break;
+        case 64: if constexpr (backward_serves(K, 64)) return backward_map<IO, K, 64>(a, s); break;
     }
     return fail(MIRA_DECLINE, "mira: no backward kernel for this d_m");
 }
