@@ -145,6 +145,10 @@ def test_backward_plan_and_errors(lib):
     # no forward workspace over several chunks: bad argument
     assert lib.mira_lattice_backward(*args, *grads, *tail, null, 0, fake, 1 << 30, null) == 2
     assert b"forward" in lib.mira_last_error()
+    # a workspace off a 16-byte boundary: bad argument (the reduce reads it 16 bytes at a time)
+    assert lib.mira_lattice_backward(*args, *grads, *tail, fake, 1 << 30, ctypes.c_void_p(264),
+                                     1 << 30, null) == 2
+    assert b"aligned" in lib.mira_last_error()
     # a (K, d_m) without backward kernels declines
     tail_wide = [2, 100, 64, 2, 128, 0, 6]
     wide_args = list(args)
